@@ -1,0 +1,582 @@
+// forge_sort.cpp -- host runtime behind include/forge_sort.h.
+//
+// Replaces forge-sort's Metal plumbing (src/metal_helpers.rs: device/queue
+// init :206-217, PSO cache :78-146, shared buffers :194-202) and the encoders
+// of src/lib.rs (dispatch_sort :285-409, encode_sort_pipeline_full
+// :1520-1639, encode_sort_pipeline_64 :1302-1478) with HIP: one device, one
+// stream, the gfx950 code object loaded by hipModuleLoad, grow-only scratch
+// in HBM, and a fixed launch sequence per sort:
+//   fs_upsweep -> fs_plan -> fs_onesweep x digits -> fs_finish
+// The sequence never reads anything back to the host, so fs_encode is fully
+// asynchronous; which digit passes really run is decided on the device.
+//
+// Every HIP error is mapped to a status code and a message; nothing panics or
+// throws across the C ABI.
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/forge_sort.h"
+#include "fs_params.h"
+
+namespace {
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+
+struct ProfEntry {
+    const char* name;
+    hipEvent_t start, stop;
+};
+
+const char* const kKernelNames[] = {
+    "fs_upsweep_k32", "fs_upsweep_k64", "fs_plan",   "fs_onesweep_k32", "fs_onesweep_k32_v",
+    "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_finish", "fs_iota",
+};
+enum {
+    K_UP32, K_UP64, K_PLAN, K_OS32, K_OS32V, K_OS64, K_OS64V, K_FINISH, K_IOTA, K_COUNT
+};
+
+}  // namespace
+
+struct fs_sorter {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    hipModule_t module = nullptr;
+    hipFunction_t fn[K_COUNT] = {};
+    int num_cus = 256;
+
+    DevBuf s1k, s2k, s1v, s2v, lb0, lb1, iok, iov;
+    uint32_t* hist = nullptr;       // [FS_MAX_PORTIONS][8][256], zero between sorts
+    uint32_t* binbase = nullptr;    // [FS_MAX_PORTIONS][8][256]
+    uint32_t* tile_ctr = nullptr;   // [8]
+    FsPlan* plan = nullptr;
+    uint32_t* status = nullptr;     // pinned host word written by kernels on device errors
+
+    hipStream_t last_stream = nullptr;   // stream of the last enqueued sort
+    bool pending = false;
+
+    bool profiling = false;
+    std::vector<ProfEntry> prof;         // launches of the last sort
+    std::vector<hipEvent_t> event_pool;
+
+    std::string err;
+};
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+
+static fs_status set_err(fs_sorter* s, fs_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (s) {
+        // Display strings of SortError (lib.rs:94-104)
+        switch (st) {
+            case FS_ERR_DEVICE_NOT_FOUND: s->err = "no HIP GPU device found"; break;
+            case FS_ERR_SHADER_COMPILATION: s->err = std::string("shader compilation failed: ") + buf; break;
+            case FS_ERR_GPU_EXECUTION: s->err = std::string("GPU execution failed: ") + buf; break;
+            default: s->err = buf; break;
+        }
+    }
+    return st;
+}
+
+#define HIP_TRY(s, call)                                                                  \
+    do {                                                                                  \
+        hipError_t e_ = (call);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return set_err((s), FS_ERR_GPU_EXECUTION, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+static bool key64(fs_key_type t) { return t == FS_KEY_U64 || t == FS_KEY_I64 || t == FS_KEY_F64; }
+static size_t key_bytes(fs_key_type t) { return key64(t) ? 8 : 4; }
+static uint32_t xform_of(fs_key_type t) {
+    switch (t) {
+        case FS_KEY_I32: case FS_KEY_I64: return FS_XF_SIGN;     // lib.rs:52-57, :78-79
+        case FS_KEY_F32: case FS_KEY_F64: return FS_XF_FLOAT;    // lib.rs:60-65, :82-87
+        default: return FS_XF_NONE;
+    }
+}
+static bool valid_type(int t) { return t >= FS_KEY_U32 && t <= FS_KEY_F64; }
+
+static std::string code_object_path() {
+    const char* env = getenv("FORGE_SORT_CODE_OBJECT");
+    if (env && *env) return env;
+    Dl_info info;
+    if (dladdr((void*)&fs_sorter_new, &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t slash = p.rfind('/');
+        std::string dir = slash == std::string::npos ? "." : p.substr(0, slash);
+        return dir + "/forge_sort_gfx950.hsaco";
+    }
+    return "forge_sort_gfx950.hsaco";
+}
+
+static void free_buf(DevBuf& b) {
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.bytes = 0;
+}
+
+// Wait for any sort still in flight on a stream other than the sorter's own.
+static fs_status drain(fs_sorter* s) {
+    if (s->pending) {
+        HIP_TRY(s, hipStreamSynchronize(s->last_stream));
+        HIP_TRY(s, hipStreamSynchronize(s->stream));
+        s->pending = false;
+    }
+    return FS_OK;
+}
+
+// Grow-only device buffer (ensure_buffers*, lib.rs:1120-1289).  Growing waits
+// for in-flight work first, since that work may still use the old buffer.
+static fs_status ensure(fs_sorter* s, DevBuf& b, size_t bytes) {
+    if (b.bytes >= bytes) return FS_OK;
+    fs_status st = drain(s);
+    if (st != FS_OK) return st;
+    free_buf(b);
+    size_t want = bytes + (bytes >> 3);   // headroom against repeated small growth
+    hipError_t e = hipMalloc(&b.p, want);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        b.p = nullptr;
+        return set_err(s, FS_ERR_OUT_OF_MEMORY, "hipMalloc(%zu bytes) failed: %s", want,
+                       hipGetErrorString(e));
+    }
+    b.bytes = want;
+    return FS_OK;
+}
+
+static hipEvent_t take_event(fs_sorter* s) {
+    if (!s->event_pool.empty()) {
+        hipEvent_t e = s->event_pool.back();
+        s->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+static void recycle_profile(fs_sorter* s) {
+    for (auto& p : s->prof) {
+        if (p.start) s->event_pool.push_back(p.start);
+        if (p.stop) s->event_pool.push_back(p.stop);
+    }
+    s->prof.clear();
+}
+
+static fs_status launch(fs_sorter* s, int k, unsigned grid, unsigned block, void** args,
+                        hipStream_t st) {
+    ProfEntry pe{kKernelNames[k], nullptr, nullptr};
+    if (s->profiling) {
+        pe.start = take_event(s);
+        pe.stop = take_event(s);
+        if (pe.start) HIP_TRY(s, hipEventRecord(pe.start, st));
+    }
+    HIP_TRY(s, hipModuleLaunchKernel(s->fn[k], grid, 1, 1, block, 1, 1, 0, st, args, nullptr));
+    if (s->profiling) {
+        if (pe.stop) HIP_TRY(s, hipEventRecord(pe.stop, st));
+        s->prof.push_back(pe);
+    }
+    return FS_OK;
+}
+
+static fs_status check_device_status(fs_sorter* s) {
+    uint32_t st = __atomic_load_n(s->status, __ATOMIC_ACQUIRE);
+    if (st) {
+        __atomic_store_n(s->status, 0u, __ATOMIC_RELEASE);
+        if (st & FS_DEVERR_LOOKBACK_TIMEOUT)
+            return set_err(s, FS_ERR_GPU_EXECUTION, "look-back wait exceeded its spin bound");
+        return set_err(s, FS_ERR_GPU_EXECUTION, "device status 0x%x", st);
+    }
+    return FS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// the launch sequence
+// ---------------------------------------------------------------------------
+
+static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint32_t* vals,
+                         uint64_t n, hipStream_t st) {
+    if (!valid_type(t)) return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown key type %d", (int)t);
+    if (op != FS_OP_SORT && op != FS_OP_ARGSORT && op != FS_OP_PAIRS)
+        return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown op %d", (int)op);
+    if (n >= (1ull << 32))
+        return set_err(s, FS_ERR_INVALID_ARGUMENT, "n = %llu exceeds 2^32 - 1", (unsigned long long)n);
+    if (n > 0 && !keys) return set_err(s, FS_ERR_INVALID_ARGUMENT, "null keys");
+    if (n > 0 && op != FS_OP_SORT && !vals) return set_err(s, FS_ERR_INVALID_ARGUMENT, "null values");
+    if (s->profiling) recycle_profile(s);
+
+    if (n <= 1) {
+        // lib.rs:710-712 / :1677-1682: nothing to sort; argsort of one key is [0]
+        if (n == 1 && op == FS_OP_ARGSORT) {
+            uint64_t one = 1;
+            void* args[] = {&vals, &one};
+            fs_status r = launch(s, K_IOTA, 1, 64, args, st);
+            if (r != FS_OK) return r;
+        }
+        return FS_OK;
+    }
+
+    const size_t kb = key_bytes(t);
+    const uint32_t num_tiles = (uint32_t)((n + FS_TILE - 1) / FS_TILE);
+    fs_status r;
+    if ((r = ensure(s, s->s1k, n * kb)) != FS_OK) return r;
+    if ((r = ensure(s, s->s2k, n * kb)) != FS_OK) return r;
+    if (op != FS_OP_SORT) {
+        if ((r = ensure(s, s->s1v, n * 4)) != FS_OK) return r;
+        if (op == FS_OP_PAIRS && (r = ensure(s, s->s2v, n * 4)) != FS_OK) return r;
+    }
+    if ((r = ensure(s, s->lb0, (size_t)num_tiles * FS_RADIX * 4)) != FS_OK) return r;
+    if ((r = ensure(s, s->lb1, (size_t)num_tiles * FS_RADIX * 4)) != FS_OK) return r;
+
+    FsArgs a;
+    memset(&a, 0, sizeof a);
+    a.n = n;
+    a.key64 = key64(t) ? 1u : 0u;
+    a.xform = xform_of(t);
+    a.op = op == FS_OP_SORT ? FSK_OP_KEYS : (op == FS_OP_ARGSORT ? FSK_OP_ARGSORT : FSK_OP_PAIRS);
+    a.digits = key64(t) ? 8u : 4u;
+    a.num_tiles = num_tiles;
+    a.tiles_per_portion = FS_PORTION_KEYS / FS_TILE;
+    // upsweep: about 4 blocks per CU, each over a power-of-two number of tiles
+    // so that no block straddles a portion boundary
+    uint32_t tpb = 1;
+    while ((uint64_t)tpb * (uint64_t)s->num_cus * 4u < num_tiles) tpb <<= 1;
+    a.hist_tiles_per_block = tpb;
+    a.keys = (uint64_t)(uintptr_t)keys;
+    a.vals = (uint64_t)(uintptr_t)vals;
+    a.s1k = (uint64_t)(uintptr_t)s->s1k.p;
+    a.s2k = (uint64_t)(uintptr_t)s->s2k.p;
+    a.s1v = (uint64_t)(uintptr_t)s->s1v.p;
+    a.s2v = (uint64_t)(uintptr_t)s->s2v.p;
+    a.hist = (uint64_t)(uintptr_t)s->hist;
+    a.binbase = (uint64_t)(uintptr_t)s->binbase;
+    a.lookback0 = (uint64_t)(uintptr_t)s->lb0.p;
+    a.lookback1 = (uint64_t)(uintptr_t)s->lb1.p;
+    a.tile_ctr = (uint64_t)(uintptr_t)s->tile_ctr;
+    a.plan = (uint64_t)(uintptr_t)s->plan;
+    a.status = (uint64_t)(uintptr_t)s->status;
+
+    const unsigned up_grid = (num_tiles + tpb - 1) / tpb;
+    void* args1[] = {&a};
+    if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st)) != FS_OK) return r;
+    if ((r = launch(s, K_PLAN, 1, FS_RADIX, args1, st)) != FS_OK) return r;
+    const int os = key64(t) ? (op == FS_OP_SORT ? K_OS64 : K_OS64V) : (op == FS_OP_SORT ? K_OS32 : K_OS32V);
+    for (uint32_t d = 0; d < a.digits; ++d) {
+        uint32_t digit = d;
+        void* args2[] = {&a, &digit};
+        if ((r = launch(s, os, num_tiles, FS_BLOCK, args2, st)) != FS_OK) return r;
+    }
+    uint64_t fin_blocks = (n + 255) / 256;
+    if (fin_blocks > (uint64_t)s->num_cus * 8) fin_blocks = (uint64_t)s->num_cus * 8;
+    if ((r = launch(s, K_FINISH, (unsigned)fin_blocks, 256, args1, st)) != FS_OK) return r;
+    s->last_stream = st;
+    s->pending = true;
+    return FS_OK;
+}
+
+static fs_status sync_and_check(fs_sorter* s) {
+    if (s->pending) {
+        hipError_t e = hipStreamSynchronize(s->last_stream);
+        s->pending = false;
+        if (e != hipSuccess)
+            return set_err(s, FS_ERR_GPU_EXECUTION, "hipStreamSynchronize: %s", hipGetErrorString(e));
+    }
+    return check_device_status(s);
+}
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+
+extern "C" {
+
+const char* fs_status_str(fs_status st) {
+    switch (st) {
+        case FS_OK: return "ok";
+        case FS_ERR_DEVICE_NOT_FOUND: return "no HIP GPU device found";
+        case FS_ERR_SHADER_COMPILATION: return "shader compilation failed";
+        case FS_ERR_GPU_EXECUTION: return "GPU execution failed";
+        case FS_ERR_LENGTH_MISMATCH: return "length mismatch";
+        case FS_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case FS_ERR_OUT_OF_MEMORY: return "out of memory";
+    }
+    return "unknown status";
+}
+
+uint32_t fs_tile_keys(void) { return FS_TILE; }
+
+const char* fs_last_error(const fs_sorter* s) { return s ? s->err.c_str() : "null sorter"; }
+
+static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** out) {
+    if (!out) return FS_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0 || device < 0 || device >= count) {
+        (void)hipGetLastError();
+        return FS_ERR_DEVICE_NOT_FOUND;
+    }
+    fs_sorter* s = new (std::nothrow) fs_sorter();
+    if (!s) return FS_ERR_OUT_OF_MEMORY;
+    s->device = device;
+    fs_status r = FS_OK;
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) {
+        delete s;
+        return FS_ERR_DEVICE_NOT_FOUND;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+        s->num_cus = cus;
+    if (own) {
+        e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            delete s;
+            return FS_ERR_GPU_EXECUTION;
+        }
+        s->own_stream = true;
+    } else {
+        s->stream = stream;
+    }
+    s->last_stream = s->stream;
+
+    const std::string path = code_object_path();
+    e = hipModuleLoad(&s->module, path.c_str());
+    if (e != hipSuccess) {
+        r = set_err(s, FS_ERR_SHADER_COMPILATION, "hipModuleLoad(%s): %s", path.c_str(),
+                    hipGetErrorString(e));
+        fs_sorter_free(s);
+        return r;
+    }
+    for (int k = 0; k < K_COUNT; ++k) {
+        e = hipModuleGetFunction(&s->fn[k], s->module, kKernelNames[k]);
+        if (e != hipSuccess) {
+            fs_sorter_free(s);
+            return FS_ERR_SHADER_COMPILATION;
+        }
+    }
+    const size_t tab = (size_t)FS_MAX_PORTIONS * FS_MAX_DIGITS * FS_RADIX * 4;
+    if (hipMalloc(&s->hist, tab) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||
+        hipMalloc(&s->tile_ctr, FS_MAX_DIGITS * 4) != hipSuccess ||
+        hipMalloc(&s->plan, sizeof(FsPlan)) != hipSuccess ||
+        hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
+        fs_sorter_free(s);
+        return FS_ERR_OUT_OF_MEMORY;
+    }
+    *s->status = 0;
+    // The histogram table must start at zero; fs_plan re-zeroes it after every sort.
+    if (hipMemset(s->hist, 0, tab) != hipSuccess || hipMemset(s->tile_ctr, 0, FS_MAX_DIGITS * 4) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        fs_sorter_free(s);
+        return FS_ERR_GPU_EXECUTION;
+    }
+    *out = s;
+    return FS_OK;
+}
+
+fs_status fs_sorter_new(int device, fs_sorter** out) { return create(device, nullptr, true, out); }
+
+fs_status fs_sorter_with_context(int device, void* hip_stream, fs_sorter** out) {
+    return create(device, (hipStream_t)hip_stream, false, out);
+}
+
+void fs_sorter_free(fs_sorter* s) {
+    if (!s) return;
+    (void)hipSetDevice(s->device);
+    if (s->pending) (void)hipStreamSynchronize(s->last_stream);
+    if (s->stream || s->own_stream) (void)hipStreamSynchronize(s->stream);
+    recycle_profile(s);
+    for (hipEvent_t e : s->event_pool) (void)hipEventDestroy(e);
+    DevBuf* bufs[] = {&s->s1k, &s->s2k, &s->s1v, &s->s2v, &s->lb0, &s->lb1, &s->iok, &s->iov};
+    for (DevBuf* b : bufs) free_buf(*b);
+    if (s->hist) (void)hipFree(s->hist);
+    if (s->binbase) (void)hipFree(s->binbase);
+    if (s->tile_ctr) (void)hipFree(s->tile_ctr);
+    if (s->plan) (void)hipFree(s->plan);
+    if (s->status) (void)hipHostFree(s->status);
+    if (s->module) (void)hipModuleUnload(s->module);
+    if (s->own_stream && s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+}
+
+fs_status fs_alloc_sort_buffer(fs_sorter* s, fs_key_type type, size_t capacity, void** device_ptr) {
+    if (!s || !device_ptr) return FS_ERR_INVALID_ARGUMENT;
+    if (!valid_type(type)) return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown key type %d", (int)type);
+    *device_ptr = nullptr;
+    HIP_TRY(s, hipSetDevice(s->device));
+    size_t bytes = capacity * key_bytes(type);
+    if (bytes == 0) bytes = key_bytes(type);
+    hipError_t e = hipMalloc(device_ptr, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *device_ptr = nullptr;
+        return set_err(s, FS_ERR_OUT_OF_MEMORY, "hipMalloc(%zu bytes) failed: %s", bytes, hipGetErrorString(e));
+    }
+    return FS_OK;
+}
+
+fs_status fs_free_sort_buffer(fs_sorter* s, void* device_ptr) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    if (!device_ptr) return FS_OK;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    HIP_TRY(s, hipFree(device_ptr));
+    return FS_OK;
+}
+
+fs_status fs_copy_to_device(fs_sorter* s, void* dst, const void* src, size_t bytes) {
+    if (!s || (bytes && (!dst || !src))) return FS_ERR_INVALID_ARGUMENT;
+    if (!bytes) return FS_OK;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    HIP_TRY(s, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(s, hipStreamSynchronize(s->stream));
+    return FS_OK;
+}
+
+fs_status fs_copy_to_host(fs_sorter* s, void* dst, const void* src, size_t bytes) {
+    if (!s || (bytes && (!dst || !src))) return FS_ERR_INVALID_ARGUMENT;
+    if (!bytes) return FS_OK;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    HIP_TRY(s, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(s, hipStreamSynchronize(s->stream));
+    return FS_OK;
+}
+
+fs_status fs_encode(fs_sorter* s, fs_op op, fs_key_type type, void* device_keys, uint32_t* device_values,
+                    uint64_t n, void* hip_stream) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    HIP_TRY(s, hipSetDevice(s->device));
+    hipStream_t st = hip_stream ? (hipStream_t)hip_stream : s->stream;
+    if (s->pending && s->last_stream != st) {
+        fs_status r = drain(s);   // scratch is shared: serialise sorts issued on different streams
+        if (r != FS_OK) return r;
+    }
+    return enqueue(s, op, type, device_keys, op == FS_OP_SORT ? nullptr : device_values, n, st);
+}
+
+fs_status fs_synchronize(fs_sorter* s) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    HIP_TRY(s, hipSetDevice(s->device));
+    return sync_and_check(s);
+}
+
+fs_status fs_sort_buffer(fs_sorter* s, fs_key_type type, void* device_keys, uint64_t n) {
+    fs_status r = fs_encode(s, FS_OP_SORT, type, device_keys, nullptr, n, nullptr);
+    if (r != FS_OK) return r;
+    return sync_and_check(s);
+}
+
+fs_status fs_argsort_buffer(fs_sorter* s, fs_key_type type, const void* device_keys, uint64_t n,
+                            uint32_t* device_indices) {
+    fs_status r = fs_encode(s, FS_OP_ARGSORT, type, (void*)device_keys, device_indices, n, nullptr);
+    if (r != FS_OK) return r;
+    return sync_and_check(s);
+}
+
+fs_status fs_sort_pairs_buffer(fs_sorter* s, fs_key_type type, void* device_keys, uint32_t* device_values,
+                               uint64_t n) {
+    fs_status r = fs_encode(s, FS_OP_PAIRS, type, device_keys, device_values, n, nullptr);
+    if (r != FS_OK) return r;
+    return sync_and_check(s);
+}
+
+// Slice API: stage through the sorter's own device buffers, like the
+// reference's memcpy into buf_a (lib.rs:800-806) and back (:828-834).
+static fs_status host_op(fs_sorter* s, fs_op op, fs_key_type type, void* keys, uint32_t* vals, uint64_t n) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    if (!valid_type(type)) return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown key type %d", (int)type);
+    if (n >= (1ull << 32))
+        return set_err(s, FS_ERR_INVALID_ARGUMENT, "n = %llu exceeds 2^32 - 1", (unsigned long long)n);
+    if (n == 0) return FS_OK;
+    if (!keys || (op != FS_OP_SORT && !vals)) return set_err(s, FS_ERR_INVALID_ARGUMENT, "null pointer");
+    if (n == 1) {
+        if (op == FS_OP_ARGSORT) vals[0] = 0;
+        return FS_OK;
+    }
+    HIP_TRY(s, hipSetDevice(s->device));
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    const size_t kb = key_bytes(type);
+    if ((r = ensure(s, s->iok, n * kb)) != FS_OK) return r;
+    if (op != FS_OP_SORT && (r = ensure(s, s->iov, n * 4)) != FS_OK) return r;
+    HIP_TRY(s, hipMemcpyAsync(s->iok.p, keys, n * kb, hipMemcpyHostToDevice, s->stream));
+    if (op == FS_OP_PAIRS)
+        HIP_TRY(s, hipMemcpyAsync(s->iov.p, vals, n * 4, hipMemcpyHostToDevice, s->stream));
+    if ((r = enqueue(s, op, type, s->iok.p, (uint32_t*)s->iov.p, n, s->stream)) != FS_OK) return r;
+    if (op != FS_OP_ARGSORT)
+        HIP_TRY(s, hipMemcpyAsync(keys, s->iok.p, n * kb, hipMemcpyDeviceToHost, s->stream));
+    if (op != FS_OP_SORT)
+        HIP_TRY(s, hipMemcpyAsync(vals, s->iov.p, n * 4, hipMemcpyDeviceToHost, s->stream));
+    return sync_and_check(s);
+}
+
+fs_status fs_sort(fs_sorter* s, fs_key_type type, void* host_keys, uint64_t n) {
+    return host_op(s, FS_OP_SORT, type, host_keys, nullptr, n);
+}
+
+fs_status fs_argsort(fs_sorter* s, fs_key_type type, const void* host_keys, uint64_t n, uint32_t* host_indices) {
+    return host_op(s, FS_OP_ARGSORT, type, (void*)host_keys, host_indices, n);
+}
+
+fs_status fs_sort_pairs(fs_sorter* s, fs_key_type type, void* host_keys, uint64_t n_keys, uint32_t* host_values,
+                        uint64_t n_values) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    if (n_keys != n_values)   // lib.rs:1928-1934, checked before any GPU work
+        return set_err(s, FS_ERR_LENGTH_MISMATCH, "length mismatch: keys=%llu, values=%llu",
+                       (unsigned long long)n_keys, (unsigned long long)n_values);
+    return host_op(s, FS_OP_PAIRS, type, host_keys, host_values, n_keys);
+}
+
+fs_status fs_last_pass_info(fs_sorter* s, uint32_t* n_passes, uint32_t* digit_mask) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    FsPlan p;
+    HIP_TRY(s, hipMemcpy(&p, s->plan, sizeof p, hipMemcpyDeviceToHost));
+    if (n_passes) *n_passes = p.n_passes;
+    if (digit_mask) *digit_mask = p.digit_mask;
+    return FS_OK;
+}
+
+fs_status fs_set_profiling(fs_sorter* s, int enable) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    recycle_profile(s);
+    s->profiling = enable != 0;
+    return FS_OK;
+}
+
+int fs_profile_count(fs_sorter* s) { return s ? (int)s->prof.size() : 0; }
+
+fs_status fs_profile_read(fs_sorter* s, int index, const char** kernel_name, float* ms) {
+    if (!s || index < 0 || index >= (int)s->prof.size()) return FS_ERR_INVALID_ARGUMENT;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    const ProfEntry& p = s->prof[index];
+    if (kernel_name) *kernel_name = p.name;
+    if (ms) {
+        *ms = 0.f;
+        if (p.start && p.stop) HIP_TRY(s, hipEventElapsedTime(ms, p.start, p.stop));
+    }
+    return FS_OK;
+}
+
+}  // extern "C"

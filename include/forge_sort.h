@@ -1,0 +1,159 @@
+/*
+ * forge_sort.h -- C ABI of the MI355X (gfx950) forge-sort radix sort.
+ *
+ * Drop-in boundary for forge-sort's GpuSorter
+ * (metal-forge-compute/forge-sort/src/lib.rs).  Each entry point names the
+ * Rust API it replaces; a Rust/ctypes binding maps them 1:1.  All pointers are
+ * plain host or device addresses and all sizes are element counts unless the
+ * name says bytes.  No HIP or torch types appear here: a HIP stream is passed
+ * as `void*` (a hipStream_t; NULL = the sorter's own stream).
+ *
+ * Semantics kept from the reference:
+ *   - sorts are ascending; floats follow the IEEE total order of Rust's
+ *     f32/f64::total_cmp (-NaN < -inf < ... < -0.0 < +0.0 < ... < +inf < +NaN)
+ *     by the FloatFlip transform (shaders/sort.metal:812-868);
+ *   - n <= 1 returns FS_OK with no GPU work (lib.rs:710-712, :1677-1682);
+ *   - pairs check the lengths before any work (lib.rs:1928-1934);
+ *   - n is limited to 2^32 - 1 (u32 counts and indices, lib.rs:106-130);
+ *   - one call at a time per sorter (&mut self in Rust): not thread-safe.
+ * Stronger than the reference: argsort and pairs are stable (ties keep their
+ * original index order) and deterministic.
+ */
+#ifndef FORGE_SORT_H
+#define FORGE_SORT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* SortError (lib.rs:94-104) as status codes; the message of the last failure
+ * is available from fs_last_error(). */
+typedef enum fs_status {
+    FS_OK = 0,
+    FS_ERR_DEVICE_NOT_FOUND = 1,    /* SortError::DeviceNotFound */
+    FS_ERR_SHADER_COMPILATION = 2,  /* SortError::ShaderCompilation: code object missing or not loadable */
+    FS_ERR_GPU_EXECUTION = 3,       /* SortError::GpuExecution: any HIP runtime or kernel failure */
+    FS_ERR_LENGTH_MISMATCH = 4,     /* SortError::LengthMismatch{keys, values} */
+    FS_ERR_INVALID_ARGUMENT = 5,    /* null pointer, n >= 2^32, unknown key type (Rust's types rule these out) */
+    FS_ERR_OUT_OF_MEMORY = 6        /* allocation failure (the reference panics, metal_helpers.rs:194-202) */
+} fs_status;
+
+/* SortKey implementations (lib.rs:42-88). */
+typedef enum fs_key_type {
+    FS_KEY_U32 = 0,
+    FS_KEY_I32 = 1,
+    FS_KEY_F32 = 2,
+    FS_KEY_U64 = 3,
+    FS_KEY_I64 = 4,
+    FS_KEY_F64 = 5
+} fs_key_type;
+
+/* Operation for fs_encode (the three families of GpuSorter calls). */
+typedef enum fs_op {
+    FS_OP_SORT = 0,      /* sort_<t> / sort_buffer: keys in place */
+    FS_OP_ARGSORT = 1,   /* argsort_<t>: keys untouched, u32 indices out */
+    FS_OP_PAIRS = 2      /* sort_pairs_<t>: keys and u32 values in place */
+} fs_op;
+
+/* GpuSorter (lib.rs:132-154): device, stream, loaded code object, grow-only scratch. */
+typedef struct fs_sorter fs_sorter;
+
+/* ---- construction ---------------------------------------------------------- */
+
+/* GpuSorter::new (lib.rs:596-599).  Uses HIP device `device` and a stream the
+ * sorter owns.  Loads the gfx950 code object (hipModuleLoad). */
+fs_status fs_sorter_new(int device, fs_sorter **out);
+
+/* GpuSorter::with_context (lib.rs:606-686).  Uses the caller's HIP stream
+ * (`hip_stream`, not owned; NULL = the default stream) on `device`. */
+fs_status fs_sorter_with_context(int device, void *hip_stream, fs_sorter **out);
+
+/* Drop for GpuSorter: frees scratch, unloads the module, destroys an owned stream. */
+void fs_sorter_free(fs_sorter *s);
+
+/* The message of the last failing call (SortError's Display text, lib.rs:94-104). */
+const char *fs_last_error(const fs_sorter *s);
+
+/* Display text of a status code. */
+const char *fs_status_str(fs_status st);
+
+/* ---- SortBuffer (lib.rs:160-281, alloc_sort_buffer :694-702) --------------- */
+
+/* alloc_sort_buffer<T>(capacity): device memory for `capacity` keys of `type`. */
+fs_status fs_alloc_sort_buffer(fs_sorter *s, fs_key_type type, size_t capacity, void **device_ptr);
+
+/* Drop for SortBuffer<T>. */
+fs_status fs_free_sort_buffer(fs_sorter *s, void *device_ptr);
+
+/* SortBuffer::copy_from_slice (lib.rs:213-228): host -> device, synchronous. */
+fs_status fs_copy_to_device(fs_sorter *s, void *device_dst, const void *host_src, size_t bytes);
+
+/* SortBuffer::copy_to_slice / as_slice (lib.rs:195-241): device -> host, synchronous. */
+fs_status fs_copy_to_host(fs_sorter *s, void *host_dst, const void *device_src, size_t bytes);
+
+/* ---- slice API: host arrays (copies in and out, like lib.rs:791-838) ------- */
+
+/* sort_u32 :791, sort_i32 :840, sort_f32 :920, sort_u64 :2238, sort_i64 :2348, sort_f64 :2417 */
+fs_status fs_sort(fs_sorter *s, fs_key_type type, void *host_keys, uint64_t n);
+
+/* argsort_u32 :1675, argsort_i32 :1754, argsort_f32 :1838, argsort_u64 :2595,
+ * argsort_i64 :2669, argsort_f64 :2747.  host_indices receives n u32 indices. */
+fs_status fs_argsort(fs_sorter *s, fs_key_type type, const void *host_keys, uint64_t n,
+                     uint32_t *host_indices);
+
+/* sort_pairs_u32 :1923, sort_pairs_i32 :2024, sort_pairs_f32 :2132,
+ * sort_pairs_u64 :2826, sort_pairs_i64 :2921 (f64 accepted as well). */
+fs_status fs_sort_pairs(fs_sorter *s, fs_key_type type, void *host_keys, uint64_t n_keys,
+                        uint32_t *host_values, uint64_t n_values);
+
+/* ---- device-resident API ----------------------------------------------------- */
+
+/* sort_buffer :708 (u32), sort_i32_buffer :1060, sort_f32_buffer :1000,
+ * sort_u64_buffer :2301, sort_i64_buffer :2486, sort_f64_buffer :2540.
+ * Sorts `n` keys at device_keys in place and waits for completion. */
+fs_status fs_sort_buffer(fs_sorter *s, fs_key_type type, void *device_keys, uint64_t n);
+
+/* Device-resident argsort (the reference only has the slice form): indices of
+ * the stable ascending order into device_indices; keys are not modified. */
+fs_status fs_argsort_buffer(fs_sorter *s, fs_key_type type, const void *device_keys, uint64_t n,
+                            uint32_t *device_indices);
+
+/* Device-resident pairs sort (the reference only has the slice form). */
+fs_status fs_sort_pairs_buffer(fs_sorter *s, fs_key_type type, void *device_keys,
+                               uint32_t *device_values, uint64_t n);
+
+/* encode_sort (lib.rs:749-785), generalised to every op and key type: enqueue
+ * the sort on `hip_stream` (NULL = the sorter's stream) and return without
+ * waiting.  For FS_OP_ARGSORT `device_values` is the index output and
+ * `device_keys` is read only; for FS_OP_SORT `device_values` is ignored.
+ * Errors detected on the device are reported by the next fs_synchronize. */
+fs_status fs_encode(fs_sorter *s, fs_op op, fs_key_type type, void *device_keys,
+                    uint32_t *device_values, uint64_t n, void *hip_stream);
+
+/* Wait for the sorter's stream (and the last encode's stream); report device errors. */
+fs_status fs_synchronize(fs_sorter *s);
+
+/* ---- introspection -------------------------------------------------------------- */
+
+/* Facts about the last completed sort: number of digit passes that ran and the
+ * bitmask of digit positions that were not constant (the rest were skipped). */
+fs_status fs_last_pass_info(fs_sorter *s, uint32_t *n_passes, uint32_t *digit_mask);
+
+/* Kernel timing: when enabled, every launch is bracketed by HIP events on its
+ * stream; fs_profile_read returns the durations (ms) of the launches of the
+ * last sort after it has completed.  Names are kernel symbols. */
+fs_status fs_set_profiling(fs_sorter *s, int enable);
+int fs_profile_count(fs_sorter *s);
+fs_status fs_profile_read(fs_sorter *s, int index, const char **kernel_name, float *ms);
+
+/* Keys per tile of the digit pass kernel and the compiled-in sizes. */
+uint32_t fs_tile_keys(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FORGE_SORT_H */

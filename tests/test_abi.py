@@ -1,0 +1,58 @@
+"""CPU-side checks of the C-ABI library: it loads, exports every symbol that
+include/forge_sort.h declares, and its host-only paths behave (no GPU here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "forge_sort.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fs_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_api():
+    names = declared_functions()
+    for required in ("fs_sorter_new", "fs_sorter_with_context", "fs_sort", "fs_argsort",
+                     "fs_sort_pairs", "fs_sort_buffer", "fs_encode", "fs_alloc_sort_buffer"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from forge_sort import _build
+    lib = ctypes.CDLL(_build.SO)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_code_object_is_gfx950():
+    from forge_sort import _build
+    blob = open(_build.HSACO, "rb").read()
+    # hipcc --genco writes a clang offload bundle holding the gfx950 ELF
+    assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+    assert b"gfx950" in blob
+    for k in (b"fs_upsweep_k32", b"fs_plan", b"fs_onesweep_k32", b"fs_onesweep_k64_v", b"fs_finish"):
+        assert k in blob
+
+
+def test_status_strings_match_sort_error_display():
+    import forge_sort
+    L = forge_sort._load()
+    assert L.fs_status_str(4) == b"length mismatch"
+    assert L.fs_status_str(3) == b"GPU execution failed"
+    assert L.fs_tile_keys() == 4096
+
+
+def test_no_device_is_reported_not_raised_as_crash():
+    """Without a GPU (this container), construction fails with DeviceNotFound."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    from forge_sort import DeviceNotFound, GpuSorter
+    with pytest.raises(DeviceNotFound):
+        GpuSorter.new()

@@ -1,0 +1,270 @@
+"""Parity of the HIP path with the CPU oracle, through the C ABI.
+
+Keys must be bit-identical to the oracle's sort; argsort indices and pair
+values must be identical to the oracle's stable order (ties by original
+index).  Covers the reference suite's cases (tests/golden/), its edge cases
+(empty, single, all-equal, sorted, reversed, non-tile-aligned, sub-tile,
+NaN/inf/-0.0/subnormals, byte-isolated 64-bit values) and every
+BASELINE.json configuration at full size.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from forge_sort import datagen
+
+pytestmark = pytest.mark.gpu
+
+BITS = {"u32": np.uint32, "i32": np.uint32, "f32": np.uint32,
+        "u64": np.uint64, "i64": np.uint64, "f64": np.uint64}
+NP = oracle.NP_DTYPES
+KINDS = ["u32", "i32", "f32", "u64", "i64", "f64"]
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "golden.json")
+
+
+@pytest.fixture(scope="module")
+def sorter():
+    from forge_sort import GpuSorter
+    s = GpuSorter.new()
+    yield s
+    s.close()
+
+
+def bits_equal(a, b, kind):
+    return np.array_equal(np.asarray(a).view(BITS[kind]), np.asarray(b).view(BITS[kind]))
+
+
+def first_diff(a, b, kind):
+    x, y = np.asarray(a).view(BITS[kind]), np.asarray(b).view(BITS[kind])
+    idx = np.nonzero(x != y)[0]
+    return None if idx.size == 0 else (int(idx[0]), hex(int(x[idx[0]])), hex(int(y[idx[0]])))
+
+
+def check_sort(sorter, kind, keys):
+    exp = oracle.sort(kind, keys)
+    got = keys.copy()
+    getattr(sorter, f"sort_{kind}")(got)
+    assert bits_equal(got, exp, kind), first_diff(got, exp, kind)
+
+
+def check_argsort(sorter, kind, keys):
+    exp = oracle.argsort(kind, keys)
+    before = keys.copy()
+    got = getattr(sorter, f"argsort_{kind}")(keys)
+    assert np.array_equal(got, exp), first_diff(got, exp, "u32")
+    assert bits_equal(keys, before, kind), "argsort modified its input"
+
+
+def check_pairs(sorter, kind, keys, vals):
+    ek, ev = oracle.sort_pairs(kind, keys, vals)
+    gk, gv = keys.copy(), vals.copy()
+    getattr(sorter, f"sort_pairs_{kind}")(gk, gv)
+    assert bits_equal(gk, ek, kind), first_diff(gk, ek, kind)
+    assert np.array_equal(gv, ev), first_diff(gv, ev, "u32")
+
+
+def check_buffer(sorter, kind, keys):
+    exp = oracle.sort(kind, keys)
+    buf = sorter.alloc_sort_buffer(kind, max(1, keys.size))
+    buf.copy_from_slice(keys)
+    fn = "sort_buffer" if kind == "u32" else f"sort_{kind}_buffer"
+    getattr(sorter, fn)(buf)
+    got = buf.as_slice()
+    buf.free()
+    assert bits_equal(got, exp, kind), first_diff(got, exp, kind)
+
+
+# ---- golden vectors from the reference tests ---------------------------------
+
+def load_golden():
+    with open(GOLDEN) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("case", load_golden(), ids=lambda c: c["name"])
+def test_golden(sorter, case):
+    kind = case["type"]
+    keys = np.array(case["keys"], dtype=BITS[kind]).view(NP[kind])
+    if case["op"] == "sort":
+        got = keys.copy()
+        getattr(sorter, f"sort_{kind}")(got)
+        assert got.view(BITS[kind]).tolist() == case["expected_keys"]
+        check_buffer(sorter, kind, keys)
+    elif case["op"] == "argsort":
+        assert getattr(sorter, f"argsort_{kind}")(keys).tolist() == case["expected_indices"]
+    else:
+        k, v = keys.copy(), np.array(case["values"], dtype=np.uint32)
+        getattr(sorter, f"sort_pairs_{kind}")(k, v)
+        assert k.view(BITS[kind]).tolist() == case["expected_keys"]
+        assert v.tolist() == case["expected_values"]
+
+
+# ---- edge cases and sizes ------------------------------------------------------
+
+def make_keys(kind, n, dist, seed):
+    g = np.random.Generator(np.random.PCG64(seed))
+    wide = BITS[kind] == np.uint64
+    hi = 1 << (64 if wide else 32)
+    if dist == "uniform":
+        b = g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False)
+    elif dist == "zeros":
+        b = np.zeros(n, dtype=BITS[kind])
+    elif dist == "same":
+        b = np.full(n, 0xDEADBEEF, dtype=BITS[kind])
+    elif dist == "sorted":
+        b = np.sort(g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False))
+    elif dist == "reverse":
+        b = np.sort(g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False))[::-1].copy()
+    elif dist == "few":
+        b = g.choice(g.integers(0, hi, size=7, dtype=BITS[kind], endpoint=False), size=n)
+    elif dist == "lowbits":
+        b = g.integers(0, 1 << 12, size=n, dtype=BITS[kind])
+    else:
+        raise ValueError(dist)
+    keys = b.view(NP[kind])
+    if kind in ("f32", "f64") and dist == "uniform" and n >= 16:
+        specials = ([0x7FC00000, 0xFFC00001, 0x7F800000, 0xFF800000, 0, 0x80000000, 1, 0x80000001]
+                    if kind == "f32" else
+                    [0x7FF8000000000000, 0xFFF8000000000001, 0x7FF0000000000000,
+                     0xFFF0000000000000, 0, 1 << 63, 1, (1 << 63) | 1])
+        pos = g.choice(n, size=min(n, 64), replace=False)
+        keys.view(BITS[kind])[pos] = np.array(specials, dtype=BITS[kind])[np.arange(pos.size) % 8]
+    return keys
+
+
+SIZES = [2, 3, 100, 255, 4095, 4096, 4097, 65543, 1_000_000]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n", SIZES)
+def test_sort_sizes(sorter, kind, n):
+    check_sort(sorter, kind, make_keys(kind, n, "uniform", seed=n))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dist", ["zeros", "same", "sorted", "reverse", "few", "lowbits"])
+def test_sort_distributions(sorter, kind, dist):
+    check_sort(sorter, kind, make_keys(kind, 100_003, dist, seed=7))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n", [2, 100, 4097, 65543, 1_000_000])
+def test_argsort_sizes(sorter, kind, n):
+    check_argsort(sorter, kind, make_keys(kind, n, "uniform", seed=100 + n))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dist", ["same", "few", "lowbits", "reverse"])
+def test_argsort_ties(sorter, kind, dist):
+    check_argsort(sorter, kind, make_keys(kind, 70_001, dist, seed=11))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n", [2, 100, 4097, 1_000_000])
+@pytest.mark.parametrize("dist", ["uniform", "few"])
+def test_pairs(sorter, kind, n, dist):
+    keys = make_keys(kind, n, dist, seed=200 + n)
+    vals = np.random.Generator(np.random.PCG64(n)).integers(0, 1 << 32, size=n, dtype=np.uint32)
+    check_pairs(sorter, kind, keys, vals)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n", [0, 1])
+def test_trivial_lengths(sorter, kind, n):
+    keys = make_keys(kind, 2, "uniform", seed=1)[:n].copy()
+    check_sort(sorter, kind, keys)
+    assert getattr(sorter, f"argsort_{kind}")(keys).tolist() == list(range(n))
+    vals = np.arange(n, dtype=np.uint32)
+    getattr(sorter, f"sort_pairs_{kind}")(keys, vals)
+    assert vals.tolist() == list(range(n))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_sort_buffer(sorter, kind):
+    for n in (2, 4097, 300_007):
+        check_buffer(sorter, kind, make_keys(kind, n, "uniform", seed=n + 3))
+
+
+def test_length_mismatch_before_gpu_work(sorter):
+    from forge_sort import LengthMismatch
+    with pytest.raises(LengthMismatch, match="length mismatch: keys=3, values=2"):
+        sorter.sort_pairs_u32(np.array([1, 2, 3], np.uint32), np.array([10, 20], np.uint32))
+
+
+def test_buffer_reuse_and_interleaving(sorter):
+    """regression.rs: one sorter across types and sizes, grow-only scratch reused."""
+    for n, kind in [(1_000_000, "u32"), (1000, "f64"), (2_000_000, "i32"), (100, "u32"),
+                    (500_000, "u64"), (3, "f32"), (1_500_000, "i64")]:
+        check_sort(sorter, kind, make_keys(kind, n, "uniform", seed=n))
+        check_argsort(sorter, kind, make_keys(kind, n // 2 + 2, "few", seed=n))
+
+
+def test_deterministic(sorter):
+    keys = make_keys("f32", 2_000_000, "few", seed=5)
+    a = sorter.argsort_f32(keys)
+    b = sorter.argsort_f32(keys)
+    assert np.array_equal(a, b)
+
+
+def test_constant_digit_passes_skipped(sorter):
+    keys = datagen.low20_u64(1_000_000, high=0x123456789AB)
+    check_sort(sorter, "u64", keys)
+    passes, mask = sorter.last_pass_info()
+    assert passes == 3 and mask == 0b111
+
+
+def test_encode_sort_async(sorter):
+    keys = make_keys("u32", 1_000_003, "uniform", seed=9)
+    buf = sorter.alloc_sort_buffer("u32", keys.size)
+    buf.copy_from_slice(keys)
+    sorter.encode_sort(buf)
+    sorter.synchronize()
+    assert bits_equal(buf.as_slice(), oracle.sort("u32", keys), "u32")
+    buf.free()
+
+
+# ---- BASELINE.json configurations at full size ------------------------------------
+
+def test_config0_sort_u32_1m(sorter):
+    check_sort(sorter, "u32", datagen.uniform_u32(1 << 20, seed=101))
+
+
+@pytest.mark.parametrize("n", [16_777_216, 16_000_000, 268_435_456])
+def test_config1_sort_buffer_u32(sorter, n):
+    check_buffer(sorter, "u32", datagen.uniform_u32(n, seed=102))
+
+
+def test_config2_sort_f32_specials(sorter):
+    keys = datagen.f32_normal_specials(1 << 26, seed=103)
+    check_sort(sorter, "f32", keys)
+
+
+def test_config2_sort_i32(sorter):
+    check_sort(sorter, "i32", datagen.uniform_i32(1 << 26, seed=104))
+
+
+def test_config3_argsort_f32_ties(sorter):
+    check_argsort(sorter, "f32", datagen.argsort_f32_ties(1 << 24, seed=105))
+
+
+def test_config3_pairs_zipf(sorter):
+    keys, vals = datagen.zipf_pairs_u32(1 << 26, seed=106)
+    check_pairs(sorter, "u32", keys, vals)
+
+
+@pytest.mark.parametrize("kind", ["u64", "i64", "f64", "low20_zero", "low20_const"])
+def test_config4_64bit(sorter, kind):
+    n = 134_217_728
+    if kind == "u64":
+        check_buffer(sorter, "u64", datagen.uniform_u64(n, seed=107))
+    elif kind == "i64":
+        check_buffer(sorter, "i64", datagen.uniform_i64(n, seed=108))
+    elif kind == "f64":
+        check_buffer(sorter, "f64", datagen.normal_f64(n, seed=109))
+    elif kind == "low20_zero":
+        check_buffer(sorter, "u64", datagen.low20_u64(n, high=0, seed=110))
+    else:
+        check_buffer(sorter, "u64", datagen.low20_u64(n, high=0xABCDEF01234, seed=111))
