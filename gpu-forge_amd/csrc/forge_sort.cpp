@@ -66,7 +66,7 @@ struct fs_sorter {
     bool pending = false;
 
     bool profiling = false;
-    std::vector<ProfEntry> prof;         // launches of the last sort
+    std::vector<ProfEntry> prof;         // launches since profiling was enabled or reset
     std::vector<hipEvent_t> event_pool;
 
     std::string err;
@@ -219,7 +219,6 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         return set_err(s, FS_ERR_INVALID_ARGUMENT, "n = %llu exceeds 2^32 - 1", (unsigned long long)n);
     if (n > 0 && !keys) return set_err(s, FS_ERR_INVALID_ARGUMENT, "null keys");
     if (n > 0 && op != FS_OP_SORT && !vals) return set_err(s, FS_ERR_INVALID_ARGUMENT, "null values");
-    if (s->profiling) recycle_profile(s);
 
     if (n <= 1) {
         // lib.rs:710-712 / :1677-1682: nothing to sort; argsort of one key is [0]
@@ -561,6 +560,14 @@ fs_status fs_set_profiling(fs_sorter* s, int enable) {
     if (r != FS_OK) return r;
     recycle_profile(s);
     s->profiling = enable != 0;
+    return FS_OK;
+}
+
+fs_status fs_profile_reset(fs_sorter* s) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    recycle_profile(s);
     return FS_OK;
 }
 

@@ -122,6 +122,7 @@ def _load():
         "fs_last_pass_info": ([vp, u32p, u32p], i),
         "fs_set_profiling": ([vp, i], i),
         "fs_profile_count": ([vp], i),
+        "fs_profile_reset": ([vp], i),
         "fs_profile_read": ([vp, i, ctypes.POINTER(ctypes.c_char_p),
                              ctypes.POINTER(ctypes.c_float)], i),
         "fs_tile_keys": ([], ctypes.c_uint32),
@@ -401,8 +402,11 @@ class GpuSorter:
     def set_profiling(self, enable):
         self._check(_load().fs_set_profiling(self._h, 1 if enable else 0))
 
+    def profile_reset(self):
+        self._check(_load().fs_profile_reset(self._h))
+
     def profile(self):
-        """[(kernel name, ms)] of the launches of the last sort (profiling on)."""
+        """[(kernel name, ms)] of every launch since profiling was enabled or reset."""
         L = _load()
         out = []
         for i in range(L.fs_profile_count(self._h)):

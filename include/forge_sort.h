@@ -142,10 +142,13 @@ fs_status fs_synchronize(fs_sorter *s);
  * bitmask of digit positions that were not constant (the rest were skipped). */
 fs_status fs_last_pass_info(fs_sorter *s, uint32_t *n_passes, uint32_t *digit_mask);
 
-/* Kernel timing: when enabled, every launch is bracketed by HIP events on its
- * stream; fs_profile_read returns the durations (ms) of the launches of the
- * last sort after it has completed.  Names are kernel symbols. */
+/* Kernel timing (the role of forge-primitives' GpuTimer, timing.rs:40-48):
+ * when enabled, every launch is bracketed by HIP events on the stream it runs
+ * on.  Launches accumulate until fs_profile_reset (or re-enabling);
+ * fs_profile_read waits for them and returns each launch's kernel symbol and
+ * duration in ms. */
 fs_status fs_set_profiling(fs_sorter *s, int enable);
+fs_status fs_profile_reset(fs_sorter *s);
 int fs_profile_count(fs_sorter *s);
 fs_status fs_profile_read(fs_sorter *s, int index, const char **kernel_name, float *ms);
 
