@@ -53,6 +53,8 @@ struct fs_sorter {
     bool own_stream = false;
     hipModule_t module = nullptr;
     hipFunction_t fn[K_COUNT] = {};
+    uint32_t tile[4] = {};          // keys per tile of each digit-pass variant (FS_VAR_*)
+    uint32_t block[4] = {};         // threads per block of each variant
     int num_cus = 256;
 
     DevBuf s1k, s2k, s1v, s2v, lb0, lb1, iok, iov;
@@ -232,7 +234,12 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     }
 
     const size_t kb = key_bytes(t);
-    const uint32_t num_tiles = (uint32_t)((n + FS_TILE - 1) / FS_TILE);
+    if ((uintptr_t)keys % kb != 0 || (vals && (uintptr_t)vals % 4 != 0))
+        return set_err(s, FS_ERR_INVALID_ARGUMENT, "misaligned key or value pointer");
+    const int var = key64(t) ? (op == FS_OP_SORT ? FS_VAR_K64 : FS_VAR_K64V)
+                             : (op == FS_OP_SORT ? FS_VAR_K32 : FS_VAR_K32V);
+    const uint32_t tile = s->tile[var];
+    const uint32_t num_tiles = (uint32_t)((n + tile - 1) / tile);
     fs_status r;
     if ((r = ensure(s, s->s1k, n * kb)) != FS_OK) return r;
     if ((r = ensure(s, s->s2k, n * kb)) != FS_OK) return r;
@@ -251,11 +258,16 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.op = op == FS_OP_SORT ? FSK_OP_KEYS : (op == FS_OP_ARGSORT ? FSK_OP_ARGSORT : FSK_OP_PAIRS);
     a.digits = key64(t) ? 8u : 4u;
     a.num_tiles = num_tiles;
-    a.tiles_per_portion = FS_PORTION_KEYS / FS_TILE;
+    // portions: the largest power-of-two tile count holding at most 2^30 keys
+    uint32_t tpp = 1;
+    while ((uint64_t)tpp * 2u * tile <= FS_PORTION_KEYS) tpp <<= 1;
+    a.tiles_per_portion = tpp;
+    a.tile = tile;
+    a.vec_ok = ((uintptr_t)keys % 16 == 0) ? 1u : 0u;
     // upsweep: about 4 blocks per CU, each over a power-of-two number of tiles
-    // so that no block straddles a portion boundary
+    // (so that no block straddles a portion boundary)
     uint32_t tpb = 1;
-    while ((uint64_t)tpb * (uint64_t)s->num_cus * 4u < num_tiles) tpb <<= 1;
+    while ((uint64_t)tpb * (uint64_t)s->num_cus * 4u < num_tiles && tpb < tpp) tpb <<= 1;
     a.hist_tiles_per_block = tpb;
     a.keys = (uint64_t)(uintptr_t)keys;
     a.vals = (uint64_t)(uintptr_t)vals;
@@ -275,11 +287,11 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     void* args1[] = {&a};
     if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st)) != FS_OK) return r;
     if ((r = launch(s, K_PLAN, 1, FS_RADIX, args1, st)) != FS_OK) return r;
-    const int os = key64(t) ? (op == FS_OP_SORT ? K_OS64 : K_OS64V) : (op == FS_OP_SORT ? K_OS32 : K_OS32V);
+    const int os = K_OS32 + var;   // kernel order matches FS_VAR_*
     for (uint32_t d = 0; d < a.digits; ++d) {
         uint32_t digit = d;
         void* args2[] = {&a, &digit};
-        if ((r = launch(s, os, num_tiles, FS_BLOCK, args2, st)) != FS_OK) return r;
+        if ((r = launch(s, os, num_tiles, s->block[var], args2, st)) != FS_OK) return r;
     }
     uint64_t fin_blocks = (n + 255) / 256;
     if (fin_blocks > (uint64_t)s->num_cus * 8) fin_blocks = (uint64_t)s->num_cus * 8;
@@ -318,7 +330,11 @@ const char* fs_status_str(fs_status st) {
     return "unknown status";
 }
 
-uint32_t fs_tile_keys(void) { return FS_TILE; }
+fs_status fs_tile_config(const fs_sorter* s, uint32_t keys_per_tile[4]) {
+    if (!s || !keys_per_tile) return FS_ERR_INVALID_ARGUMENT;
+    for (int i = 0; i < 4; ++i) keys_per_tile[i] = s->tile[i];
+    return FS_OK;
+}
 
 const char* fs_last_error(const fs_sorter* s) { return s ? s->err.c_str() : "null sorter"; }
 
@@ -368,6 +384,23 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
             fs_sorter_free(s);
             return FS_ERR_SHADER_COMPILATION;
         }
+    }
+    {
+        // tile geometry compiled into the code object
+        hipDeviceptr_t gp = nullptr, bp = nullptr;
+        size_t gsz = 0, bsz = 0;
+        if (hipModuleGetGlobal(&gp, &gsz, s->module, "fs_tile_config") != hipSuccess || gsz != 16 ||
+            hipModuleGetGlobal(&bp, &bsz, s->module, "fs_block_config") != hipSuccess || bsz != 16 ||
+            hipMemcpyDtoH(s->tile, gp, 16) != hipSuccess || hipMemcpyDtoH(s->block, bp, 16) != hipSuccess) {
+            r = set_err(s, FS_ERR_SHADER_COMPILATION, "code object lacks fs_tile_config/fs_block_config");
+            fs_sorter_free(s);
+            return r;
+        }
+        for (int i = 0; i < 4; ++i)
+            if (s->tile[i] == 0 || s->block[i] < FS_RADIX) {
+                fs_sorter_free(s);
+                return FS_ERR_SHADER_COMPILATION;
+            }
     }
     const size_t tab = (size_t)FS_MAX_PORTIONS * FS_MAX_DIGITS * FS_RADIX * 4;
     if (hipMalloc(&s->hist, tab) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||

@@ -10,10 +10,43 @@
 #define FS_RADIX 256
 #define FS_MAX_DIGITS 8
 
-// Onesweep tile: FS_BLOCK threads (wave64 x FS_BLOCK/64) x FS_ITEMS keys.
-#define FS_BLOCK 256
-#define FS_ITEMS 16
-#define FS_TILE (FS_BLOCK * FS_ITEMS)
+// Digit-pass tiles: BLOCK threads (BLOCK/64 wave64s) x ITEMS keys per thread,
+// per kernel variant.  The host reads the tile sizes from the code object
+// (fs_tile_config), so they are only defined here.
+#ifndef FS_K32_BLOCK
+#define FS_K32_BLOCK 512
+#endif
+#ifndef FS_K32_ITEMS
+#define FS_K32_ITEMS 16
+#endif
+#ifndef FS_K32V_BLOCK
+#define FS_K32V_BLOCK 256
+#endif
+#ifndef FS_K32V_ITEMS
+#define FS_K32V_ITEMS 16
+#endif
+#ifndef FS_K64_BLOCK
+#define FS_K64_BLOCK 256
+#endif
+#ifndef FS_K64_ITEMS
+#define FS_K64_ITEMS 16
+#endif
+#ifndef FS_K64V_BLOCK
+#define FS_K64V_BLOCK 256
+#endif
+#ifndef FS_K64V_ITEMS
+#define FS_K64V_ITEMS 12
+#endif
+// Ranking inside a wave: 0 = ballot match (8 ballots per key),
+// 1 = LDS atomic-OR lane masks.
+#ifndef FS_RANK_MODE
+#define FS_RANK_MODE 0
+#endif
+// index into fs_tile_config
+#define FS_VAR_K32 0
+#define FS_VAR_K32V 1
+#define FS_VAR_K64 2
+#define FS_VAR_K64V 3
 
 // Upsweep (all-digit histogram) block.
 #define FS_HIST_BLOCK 256
@@ -79,10 +112,12 @@ typedef struct FsArgs {
     uint32_t xform;             // FS_XF_*
     uint32_t op;                // FSK_OP_*
     uint32_t digits;            // 4 or 8
-    uint32_t num_tiles;         // ceil(n / FS_TILE)
-    uint32_t tiles_per_portion; // FS_PORTION_KEYS / FS_TILE
-    uint32_t hist_tiles_per_block;
-    uint32_t pad;
+    uint32_t num_tiles;         // ceil(n / tile)
+    uint32_t tiles_per_portion; // power of two, tiles_per_portion * tile <= FS_PORTION_KEYS
+    uint32_t hist_tiles_per_block;  // power of two dividing tiles_per_portion
+    uint32_t tile;              // keys per tile of the digit-pass variant in use
+    uint32_t vec_ok;            // keys pointer is 16-byte aligned
+    uint32_t pad2;
     uint64_t keys;              // caller keys (in place for KEYS/PAIRS; read-only for ARGSORT)
     uint64_t vals;              // caller values (PAIRS) or output indices (ARGSORT)
     uint64_t s1k, s2k, s1v, s2v;   // scratch ping-pong buffers

@@ -125,7 +125,7 @@ def _load():
         "fs_profile_reset": ([vp], i),
         "fs_profile_read": ([vp, i, ctypes.POINTER(ctypes.c_char_p),
                              ctypes.POINTER(ctypes.c_float)], i),
-        "fs_tile_keys": ([], ctypes.c_uint32),
+        "fs_tile_config": ([vp, u32p], i),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -399,6 +399,12 @@ class GpuSorter:
         self._check(_load().fs_last_pass_info(self._h, ctypes.byref(n), ctypes.byref(m)))
         return n.value, m.value
 
+    def tile_config(self):
+        """Keys per tile of the digit-pass kernels: {u32, u32+values, u64, u64+values}."""
+        t = (ctypes.c_uint32 * 4)()
+        self._check(_load().fs_tile_config(self._h, t))
+        return {"k32": t[0], "k32_v": t[1], "k64": t[2], "k64_v": t[3]}
+
     def set_profiling(self, enable):
         self._check(_load().fs_set_profiling(self._h, 1 if enable else 0))
 
@@ -416,5 +422,3 @@ class GpuSorter:
         return out
 
 
-def tile_keys():
-    return _load().fs_tile_keys()

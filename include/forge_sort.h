@@ -152,8 +152,9 @@ fs_status fs_profile_reset(fs_sorter *s);
 int fs_profile_count(fs_sorter *s);
 fs_status fs_profile_read(fs_sorter *s, int index, const char **kernel_name, float *ms);
 
-/* Keys per tile of the digit pass kernel and the compiled-in sizes. */
-uint32_t fs_tile_keys(void);
+/* Keys per tile of the digit-pass kernels compiled into the loaded code
+ * object: [u32 keys, u32 keys + values, u64 keys, u64 keys + values]. */
+fs_status fs_tile_config(const fs_sorter *s, uint32_t keys_per_tile[4]);
 
 #ifdef __cplusplus
 }
