@@ -16,6 +16,12 @@ radix sort, oracle/forge_sort_oracle.c) on the same keys on the host, and
 reports labelled C++ stand-ins for the reference bench's Rust sort_unstable
 and rayon par_sort_unstable (std::sort, __gnu_parallel::sort).
 
+Device memory, copies and synchronisation go through the library itself
+(hipMalloc / hipMemcpy / hipDeviceSynchronize behind the C ABI); torch is not
+imported, so the library runs on the ROCm HIP runtime it was built against
+rather than on the copy bundled with torch (both share one soname, and
+whichever loads first would serve both).
+
 Prints one JSON line.  --gpus > 1 is refused: this build measures one GPU.
 """
 import argparse
@@ -120,46 +126,53 @@ def main():
               "single-GPU and no multi-GPU path is built", file=sys.stderr)
         sys.exit(2)
 
-    import torch
-    if not torch.cuda.is_available():
+    from forge_sort import OP_SORT, DeviceNotFound, GpuSorter, datagen
+    try:
+        sorter = GpuSorter.new(0)
+    except DeviceNotFound:
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
-    from forge_sort import OP_SORT, GpuSorter, datagen
 
     n, K, W = args.n, args.steps, args.warmup
     log(f"bench: sort_buffer u32 n={n:,} steps={K} warmup={W}")
     keys = datagen.uniform_u32(n, seed=2024)
-    sorter = GpuSorter.new(0)
-    src = torch.from_numpy(keys.view(np.int32)).to("cuda:0")
+    src = sorter.alloc_sort_buffer("u32", n)
+    src.copy_from_slice(keys)
     bufs = []
     for _ in range(W + K):
-        b = torch.empty_like(src)
-        b.copy_(src)
+        b = sorter.alloc_sort_buffer("u32", n)
+        sorter.copy_device(b.device_ptr(), src.device_ptr(), 4 * n)
         bufs.append(b)
-    torch.cuda.synchronize()
+    sorter.device_synchronize()
 
     for i in range(W):
-        sorter.encode(OP_SORT, "u32", bufs[i].data_ptr(), None, n)
+        sorter.encode(OP_SORT, "u32", bufs[i].device_ptr(), None, n)
     sorter.synchronize()
 
     sorter.set_profiling(True)
     sorter.profile_reset()
-    torch.cuda.synchronize()
+    sorter.device_synchronize()
     t0 = time.perf_counter()
     for i in range(K):
-        sorter.encode(OP_SORT, "u32", bufs[W + i].data_ptr(), None, n)
+        sorter.encode(OP_SORT, "u32", bufs[W + i].device_ptr(), None, n)
     sorter.synchronize()
-    torch.cuda.synchronize()
+    sorter.device_synchronize()
     t1 = time.perf_counter()
     prof = sorter.profile()
     sorter.set_profiling(False)
     log(f"bench: timed {K} sorts in {t1 - t0:.4f} s")
 
-    # sanity: the last output is sorted and a permutation-invariant checksum matches
-    last = bufs[-1].to(torch.int64) & 0xFFFFFFFF
-    ok_sorted = bool((last[1:] >= last[:-1]).all().item())
-    ok_sum = int(last.sum().item()) == int(keys.astype(np.uint64).sum())
-    if not (ok_sorted and ok_sum):
+    # sanity: the last output is sorted and holds the same multiset (checksums)
+    bufs[-1].set_len(n)
+    last = bufs[-1].as_slice()
+    ok_sorted = bool(np.all(last[1:] >= last[:-1]))
+    ok_sum = int(last.astype(np.uint64).sum()) == int(keys.astype(np.uint64).sum())
+    ok_xor = int(np.bitwise_xor.reduce(last)) == int(np.bitwise_xor.reduce(keys))
+    del last
+    for b in bufs:
+        b.free()
+    src.free()
+    if not (ok_sorted and ok_sum and ok_xor):
         print("bench: output check FAILED", file=sys.stderr)
         sys.exit(3)
 

@@ -61,8 +61,10 @@ struct fs_sorter {
     uint32_t* hist = nullptr;       // [FS_MAX_PORTIONS][8][256], zero between sorts
     uint32_t* binbase = nullptr;    // [FS_MAX_PORTIONS][8][256]
     uint32_t* tile_ctr = nullptr;   // [8]
-    FsPlan* plan = nullptr;
+    uint32_t* plan = nullptr;       // u32[FS_PLAN_WORDS] device-side schedule
     uint32_t* status = nullptr;     // pinned host word written by kernels on device errors
+    unsigned long long* stats = nullptr;   // device u64[FS_STAT_COUNT]
+    bool stats_on = false;
 
     hipStream_t last_stream = nullptr;   // stream of the last enqueued sort
     bool pending = false;
@@ -201,6 +203,10 @@ static fs_status check_device_status(fs_sorter* s) {
     uint32_t st = __atomic_load_n(s->status, __ATOMIC_ACQUIRE);
     if (st) {
         __atomic_store_n(s->status, 0u, __ATOMIC_RELEASE);
+        if (st & FS_DEVERR_BAD_TILE)
+            return set_err(s, FS_ERR_GPU_EXECUTION, "digit pass drew a tile id beyond the grid");
+        if (st & FS_DEVERR_BAD_PLAN)
+            return set_err(s, FS_ERR_GPU_EXECUTION, "device schedule named an unknown buffer");
         if (st & FS_DEVERR_LOOKBACK_TIMEOUT)
             return set_err(s, FS_ERR_GPU_EXECUTION, "look-back wait exceeded its spin bound");
         return set_err(s, FS_ERR_GPU_EXECUTION, "device status 0x%x", st);
@@ -256,7 +262,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.key64 = key64(t) ? 1u : 0u;
     a.xform = xform_of(t);
     a.op = op == FS_OP_SORT ? FSK_OP_KEYS : (op == FS_OP_ARGSORT ? FSK_OP_ARGSORT : FSK_OP_PAIRS);
-    a.digits = key64(t) ? 8u : 4u;
+    a.digits = key64(t) ? 8u : 16u;
     a.num_tiles = num_tiles;
     // portions: the largest power-of-two tile count holding at most 2^30 keys
     uint32_t tpp = 1;
@@ -264,10 +270,11 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.tiles_per_portion = tpp;
     a.tile = tile;
     a.vec_ok = ((uintptr_t)keys % 16 == 0) ? 1u : 0u;
-    // upsweep: about 4 blocks per CU, each over a power-of-two number of tiles
-    // (so that no block straddles a portion boundary)
-    uint32_t tpb = 1;
-    while ((uint64_t)tpb * (uint64_t)s->num_cus * 4u < num_tiles && tpb < tpp) tpb <<= 1;
+    // upsweep: about 4 blocks per CU over contiguous runs of tiles
+    static const uint32_t up_per_cu = getenv("FS_UPSWEEP_BLOCKS_PER_CU")
+                                          ? (uint32_t)atoi(getenv("FS_UPSWEEP_BLOCKS_PER_CU")) : 16u;
+    const uint32_t up_blocks_target = (uint32_t)s->num_cus * (up_per_cu ? up_per_cu : 16u);
+    const uint32_t tpb = (num_tiles + up_blocks_target - 1) / up_blocks_target;
     a.hist_tiles_per_block = tpb;
     a.keys = (uint64_t)(uintptr_t)keys;
     a.vals = (uint64_t)(uintptr_t)vals;
@@ -282,6 +289,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.tile_ctr = (uint64_t)(uintptr_t)s->tile_ctr;
     a.plan = (uint64_t)(uintptr_t)s->plan;
     a.status = (uint64_t)(uintptr_t)s->status;
+    a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 
     const unsigned up_grid = (num_tiles + tpb - 1) / tpb;
     void* args1[] = {&a};
@@ -405,7 +413,8 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
     const size_t tab = (size_t)FS_MAX_PORTIONS * FS_MAX_DIGITS * FS_RADIX * 4;
     if (hipMalloc(&s->hist, tab) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||
         hipMalloc(&s->tile_ctr, FS_MAX_DIGITS * 4) != hipSuccess ||
-        hipMalloc(&s->plan, sizeof(FsPlan)) != hipSuccess ||
+        hipMalloc(&s->plan, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc(&s->stats, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
         fs_sorter_free(s);
         return FS_ERR_OUT_OF_MEMORY;
@@ -413,6 +422,8 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
     *s->status = 0;
     // The histogram table must start at zero; fs_plan re-zeroes it after every sort.
     if (hipMemset(s->hist, 0, tab) != hipSuccess || hipMemset(s->tile_ctr, 0, FS_MAX_DIGITS * 4) != hipSuccess ||
+        hipMemset(s->stats, 0, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
+        hipMemset(s->plan, 0, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         fs_sorter_free(s);
         return FS_ERR_GPU_EXECUTION;
@@ -440,6 +451,7 @@ void fs_sorter_free(fs_sorter* s) {
     if (s->binbase) (void)hipFree(s->binbase);
     if (s->tile_ctr) (void)hipFree(s->tile_ctr);
     if (s->plan) (void)hipFree(s->plan);
+    if (s->stats) (void)hipFree(s->stats);
     if (s->status) (void)hipHostFree(s->status);
     if (s->module) (void)hipModuleUnload(s->module);
     if (s->own_stream && s->stream) (void)hipStreamDestroy(s->stream);
@@ -489,6 +501,24 @@ fs_status fs_copy_to_host(fs_sorter* s, void* dst, const void* src, size_t bytes
     HIP_TRY(s, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s->stream));
     HIP_TRY(s, hipStreamSynchronize(s->stream));
     return FS_OK;
+}
+
+fs_status fs_copy_device(fs_sorter* s, void* dst, const void* src, size_t bytes) {
+    if (!s || (bytes && (!dst || !src))) return FS_ERR_INVALID_ARGUMENT;
+    if (!bytes) return FS_OK;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    HIP_TRY(s, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s->stream));
+    HIP_TRY(s, hipStreamSynchronize(s->stream));
+    return FS_OK;
+}
+
+fs_status fs_device_synchronize(fs_sorter* s) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    HIP_TRY(s, hipSetDevice(s->device));
+    HIP_TRY(s, hipDeviceSynchronize());
+    s->pending = false;
+    return check_device_status(s);
 }
 
 fs_status fs_encode(fs_sorter* s, fs_op op, fs_key_type type, void* device_keys, uint32_t* device_values,
@@ -580,10 +610,32 @@ fs_status fs_last_pass_info(fs_sorter* s, uint32_t* n_passes, uint32_t* digit_ma
     if (!s) return FS_ERR_INVALID_ARGUMENT;
     fs_status r = drain(s);
     if (r != FS_OK) return r;
-    FsPlan p;
-    HIP_TRY(s, hipMemcpy(&p, s->plan, sizeof p, hipMemcpyDeviceToHost));
-    if (n_passes) *n_passes = p.n_passes;
-    if (digit_mask) *digit_mask = p.digit_mask;
+    uint32_t w[FS_PLAN_WORDS];
+    HIP_TRY(s, hipMemcpy(w, s->plan, sizeof w, hipMemcpyDeviceToHost));
+    if (n_passes) *n_passes = w[FS_PLAN_NPASSES];
+    if (digit_mask) *digit_mask = w[FS_PLAN_MASK];
+    return FS_OK;
+}
+
+fs_status fs_set_lookback_stats(fs_sorter* s, int enable) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    s->stats_on = enable != 0;
+    return FS_OK;
+}
+
+fs_status fs_read_lookback_stats(fs_sorter* s, uint64_t out[4]) {
+    if (!s || !out) return FS_ERR_INVALID_ARGUMENT;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    uint64_t slots[FS_STAT_SLOTS * FS_STAT_COUNT];
+    HIP_TRY(s, hipMemcpy(slots, s->stats, sizeof slots, hipMemcpyDeviceToHost));
+    HIP_TRY(s, hipMemset(s->stats, 0, sizeof slots));
+    for (int c = 0; c < FS_STAT_COUNT; ++c) {
+        out[c] = 0;
+        for (int k = 0; k < FS_STAT_SLOTS; ++k) out[c] += slots[k * FS_STAT_COUNT + c];
+    }
     return FS_OK;
 }
 

@@ -17,7 +17,7 @@
 #define FS_K32_BLOCK 512
 #endif
 #ifndef FS_K32_ITEMS
-#define FS_K32_ITEMS 16
+#define FS_K32_ITEMS 24
 #endif
 #ifndef FS_K32V_BLOCK
 #define FS_K32V_BLOCK 256
@@ -59,7 +59,21 @@
 #define FS_LB_FLAGS 0xC0000000u
 #define FS_LB_VALUE 0x3FFFFFFFu
 #define FS_PORTION_KEYS (1u << 30)
-#define FS_MAX_PORTIONS 4
+// A portion is the largest power-of-two number of tiles holding at most 2^30
+// keys, so it holds more than 2^29 keys and n < 2^32 needs fewer than 8.
+#define FS_MAX_PORTIONS 8
+
+// Order of a tile's look-back: 2 = histogram, publish the aggregate, look back
+// and publish the inclusive prefix, then rank; 0 = rank first and publish the
+// ranking's wave counts afterwards.
+#ifndef FS_EARLY_AGG
+#define FS_EARLY_AGG 2
+#endif
+
+// Predecessor entries read per look-back round trip.
+#ifndef FS_LB_WINDOW
+#define FS_LB_WINDOW 4
+#endif
 
 // Bounded spin of a look-back wait (iterations of s_sleep(1), ~64 clocks each).
 // A predecessor tile that owns a tile id is resident and finishes in
@@ -88,22 +102,29 @@
 // Error bits reported through the host-visible status word.
 #define FS_DEVERR_LOOKBACK_TIMEOUT 1u
 
-typedef struct FsPassSched {
-    uint32_t active;       // this digit position is sorted (not constant)
-    uint32_t exec_index;   // 0..n_passes-1 among active digits
-    uint32_t flags;        // FS_PASS_*
-    uint32_t pad;
-    uint64_t src_k, dst_k, src_v, dst_v;   // device addresses
-} FsPassSched;
+// Device-side schedule written by fs_plan: FS_PLAN_WORDS u32 words, stored
+// and loaded with agent-scope (sc1) accesses.  Buffers are named by id, never
+// by address, so a kernel only ever dereferences addresses from its own
+// arguments.
+#define FS_BUF_NONE 0u
+#define FS_BUF_KEYS 1u      // caller keys
+#define FS_BUF_VALS 2u      // caller values (pairs) or output indices (argsort)
+#define FS_BUF_S1K 3u
+#define FS_BUF_S2K 4u
+#define FS_BUF_S1V 5u
+#define FS_BUF_S2V 6u
+// per digit j: word 2j   = active | exec_index << 8 | flags << 16
+//              word 2j+1 = src_k | dst_k << 8 | src_v << 16 | dst_v << 24 (buffer ids)
+#define FS_PLAN_PASS_WORDS 2
+#define FS_PLAN_NPASSES (FS_MAX_DIGITS * FS_PLAN_PASS_WORDS)      // passes that run
+#define FS_PLAN_FINISH (FS_PLAN_NPASSES + 1)                       // FS_FIN_*
+#define FS_PLAN_MASK (FS_PLAN_NPASSES + 2)                         // bit j: digit j sorted
+#define FS_PLAN_FINBUF (FS_PLAN_NPASSES + 3)                       // finish buffer ids, as word 2j+1
+#define FS_PLAN_WORDS (FS_PLAN_NPASSES + 4)
 
-typedef struct FsPlan {
-    FsPassSched pass[FS_MAX_DIGITS];
-    uint32_t n_passes;
-    uint32_t finish;       // FS_FIN_*
-    uint32_t digit_mask;   // bit j set when digit j is active
-    uint32_t pad;
-    uint64_t fin_src_k, fin_dst_k, fin_src_v, fin_dst_v;
-} FsPlan;
+// Error bits additionally reported through the status word.
+#define FS_DEVERR_BAD_TILE 2u        // a digit pass drew a tile id >= num_tiles
+#define FS_DEVERR_BAD_PLAN 4u        // a schedule named a buffer the call does not have
 
 // Kernel argument block, passed by value to every kernel.
 typedef struct FsArgs {
@@ -114,7 +135,7 @@ typedef struct FsArgs {
     uint32_t digits;            // 4 or 8
     uint32_t num_tiles;         // ceil(n / tile)
     uint32_t tiles_per_portion; // power of two, tiles_per_portion * tile <= FS_PORTION_KEYS
-    uint32_t hist_tiles_per_block;  // power of two dividing tiles_per_portion
+    uint32_t hist_tiles_per_block;  // tiles per upsweep block
     uint32_t tile;              // keys per tile of the digit-pass variant in use
     uint32_t vec_ok;            // keys pointer is 16-byte aligned
     uint32_t pad2;
@@ -125,8 +146,17 @@ typedef struct FsArgs {
     uint64_t binbase;           // u32 [FS_MAX_PORTIONS][digits][256]
     uint64_t lookback0, lookback1;  // u32 [num_tiles][256] each
     uint64_t tile_ctr;          // u32 [FS_MAX_DIGITS]
-    uint64_t plan;              // FsPlan
+    uint64_t plan;              // u32[FS_PLAN_WORDS] schedule
     uint64_t status;            // u32, host-visible error bits
+    uint64_t stats;             // u64[FS_STAT_SLOTS][FS_STAT_COUNT] look-back counters, or 0 when off
 } FsArgs;
+
+// Look-back statistics (accumulated only when FsArgs.stats is set).
+#define FS_STAT_TILES 0      // tiles that looked back
+#define FS_STAT_ROUNDS 1     // look-back round trips, summed over the 256 digits
+#define FS_STAT_STALLS 2     // rounds that found a predecessor not yet published
+#define FS_STAT_ENTRIES 3    // predecessor entries consumed
+#define FS_STAT_COUNT 4
+#define FS_STAT_SLOTS 64     // stats is u64[FS_STAT_SLOTS][FS_STAT_COUNT]
 
 #endif

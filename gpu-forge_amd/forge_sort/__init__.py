@@ -111,6 +111,8 @@ def _load():
         "fs_free_sort_buffer": ([vp, vp], i),
         "fs_copy_to_device": ([vp, vp, vp, sz], i),
         "fs_copy_to_host": ([vp, vp, vp, sz], i),
+        "fs_copy_device": ([vp, vp, vp, sz], i),
+        "fs_device_synchronize": ([vp], i),
         "fs_sort": ([vp, i, vp, u64], i),
         "fs_argsort": ([vp, i, vp, u64, vp], i),
         "fs_sort_pairs": ([vp, i, vp, u64, vp, u64], i),
@@ -126,6 +128,8 @@ def _load():
         "fs_profile_read": ([vp, i, ctypes.POINTER(ctypes.c_char_p),
                              ctypes.POINTER(ctypes.c_float)], i),
         "fs_tile_config": ([vp, u32p], i),
+        "fs_set_lookback_stats": ([vp, i], i),
+        "fs_read_lookback_stats": ([vp, ctypes.POINTER(ctypes.c_uint64)], i),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -338,6 +342,14 @@ class GpuSorter:
     def synchronize(self):
         self._check(_load().fs_synchronize(self._h))
 
+    def device_synchronize(self):
+        """Wait for everything on the device (hipDeviceSynchronize)."""
+        self._check(_load().fs_device_synchronize(self._h))
+
+    def copy_device(self, dst_ptr, src_ptr, nbytes):
+        """Device-to-device copy (e.g. restaging an unsorted input in HBM)."""
+        self._check(_load().fs_copy_device(self._h, ctypes.c_void_p(dst_ptr), ctypes.c_void_p(src_ptr), nbytes))
+
     def sort_device(self, kind, keys_ptr, n):
         self._check(_load().fs_sort_buffer(self._h, KEY_TYPES[kind], ctypes.c_void_p(keys_ptr), n))
 
@@ -404,6 +416,15 @@ class GpuSorter:
         t = (ctypes.c_uint32 * 4)()
         self._check(_load().fs_tile_config(self._h, t))
         return {"k32": t[0], "k32_v": t[1], "k64": t[2], "k64_v": t[3]}
+
+    def set_lookback_stats(self, enable):
+        self._check(_load().fs_set_lookback_stats(self._h, 1 if enable else 0))
+
+    def read_lookback_stats(self):
+        """{tiles, rounds, stalls, entries} of the decoupled look-back since the last read."""
+        c = (ctypes.c_uint64 * 4)()
+        self._check(_load().fs_read_lookback_stats(self._h, c))
+        return dict(zip(("tiles", "rounds", "stalls", "entries"), list(c)))
 
     def set_profiling(self, enable):
         self._check(_load().fs_set_profiling(self._h, 1 if enable else 0))

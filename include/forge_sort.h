@@ -94,6 +94,9 @@ fs_status fs_copy_to_device(fs_sorter *s, void *device_dst, const void *host_src
 /* SortBuffer::copy_to_slice / as_slice (lib.rs:195-241): device -> host, synchronous. */
 fs_status fs_copy_to_host(fs_sorter *s, void *host_dst, const void *device_src, size_t bytes);
 
+/* Device -> device copy of `bytes`, synchronous (staging fresh inputs in HBM). */
+fs_status fs_copy_device(fs_sorter *s, void *device_dst, const void *device_src, size_t bytes);
+
 /* ---- slice API: host arrays (copies in and out, like lib.rs:791-838) ------- */
 
 /* sort_u32 :791, sort_i32 :840, sort_f32 :920, sort_u64 :2238, sort_i64 :2348, sort_f64 :2417 */
@@ -136,6 +139,9 @@ fs_status fs_encode(fs_sorter *s, fs_op op, fs_key_type type, void *device_keys,
 /* Wait for the sorter's stream (and the last encode's stream); report device errors. */
 fs_status fs_synchronize(fs_sorter *s);
 
+/* Wait for all work on the sorter's device (hipDeviceSynchronize); report device errors. */
+fs_status fs_device_synchronize(fs_sorter *s);
+
 /* ---- introspection -------------------------------------------------------------- */
 
 /* Facts about the last completed sort: number of digit passes that ran and the
@@ -151,6 +157,13 @@ fs_status fs_set_profiling(fs_sorter *s, int enable);
 fs_status fs_profile_reset(fs_sorter *s);
 int fs_profile_count(fs_sorter *s);
 fs_status fs_profile_read(fs_sorter *s, int index, const char **kernel_name, float *ms);
+
+/* Decoupled look-back counters of the digit passes, summed over every sort
+ * since the last read: {tiles that looked back, round trips (per digit),
+ * rounds that met an unpublished predecessor, predecessor entries consumed}.
+ * Off by default; reading resets them. */
+fs_status fs_set_lookback_stats(fs_sorter *s, int enable);
+fs_status fs_read_lookback_stats(fs_sorter *s, uint64_t counters[4]);
 
 /* Keys per tile of the digit-pass kernels compiled into the loaded code
  * object: [u32 keys, u32 keys + values, u64 keys, u64 keys + values]. */
