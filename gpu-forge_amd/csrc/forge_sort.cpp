@@ -262,7 +262,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.key64 = key64(t) ? 1u : 0u;
     a.xform = xform_of(t);
     a.op = op == FS_OP_SORT ? FSK_OP_KEYS : (op == FS_OP_ARGSORT ? FSK_OP_ARGSORT : FSK_OP_PAIRS);
-    a.digits = key64(t) ? 8u : 16u;
+    a.digits = key64(t) ? 8u : 4u;     // one 8-bit digit per key byte
     a.num_tiles = num_tiles;
     // portions: the largest power-of-two tile count holding at most 2^30 keys
     uint32_t tpp = 1;
@@ -397,10 +397,10 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
         // tile geometry compiled into the code object
         hipDeviceptr_t gp = nullptr, bp = nullptr;
         size_t gsz = 0, bsz = 0;
-        if (hipModuleGetGlobal(&gp, &gsz, s->module, "fs_tile_config") != hipSuccess || gsz != 16 ||
-            hipModuleGetGlobal(&bp, &bsz, s->module, "fs_block_config") != hipSuccess || bsz != 16 ||
+        if (hipModuleGetGlobal(&gp, &gsz, s->module, "fs_kernel_tile_keys") != hipSuccess || gsz != 16 ||
+            hipModuleGetGlobal(&bp, &bsz, s->module, "fs_kernel_block_threads") != hipSuccess || bsz != 16 ||
             hipMemcpyDtoH(s->tile, gp, 16) != hipSuccess || hipMemcpyDtoH(s->block, bp, 16) != hipSuccess) {
-            r = set_err(s, FS_ERR_SHADER_COMPILATION, "code object lacks fs_tile_config/fs_block_config");
+            r = set_err(s, FS_ERR_SHADER_COMPILATION, "code object lacks fs_kernel_tile_keys/fs_kernel_block_threads");
             fs_sorter_free(s);
             return r;
         }

@@ -12,7 +12,7 @@
 
 // Digit-pass tiles: BLOCK threads (BLOCK/64 wave64s) x ITEMS keys per thread,
 // per kernel variant.  The host reads the tile sizes from the code object
-// (fs_tile_config), so they are only defined here.
+// (fs_kernel_tile_keys / fs_kernel_block_threads), so they are only defined here.
 #ifndef FS_K32_BLOCK
 #define FS_K32_BLOCK 512
 #endif
@@ -42,7 +42,7 @@
 #ifndef FS_RANK_MODE
 #define FS_RANK_MODE 0
 #endif
-// index into fs_tile_config
+// index into fs_kernel_tile_keys
 #define FS_VAR_K32 0
 #define FS_VAR_K32V 1
 #define FS_VAR_K64 2

@@ -1,0 +1,411 @@
+// hip_emu.cpp -- CPU emulation of the HIP features the forge-sort kernels and
+// host runtime use (TEST INFRASTRUCTURE ONLY; see hip/hip_runtime.h).
+//
+// Execution model:
+//  * a launch runs its blocks on a pool of OS threads (EMU_WORKERS, default 4),
+//    handed out in increasing block order, so several blocks are resident at
+//    once and the look-back between tiles is a real cross-thread race;
+//  * inside a block every GPU thread is a ucontext fiber, scheduled round-robin;
+//  * __syncthreads waits for every live thread of the block;
+//  * a wave64 operation completes once no lane of the wave is still runnable:
+//    the lanes waiting at it are the active lanes, lanes that diverged to a
+//    barrier or finished are inactive (the SIMT meaning of EXEC);
+//  * s_sleep yields; a block whose runnable threads all sleep yields its OS thread;
+//  * device allocations end on a PROT_NONE guard page (and start after one), so
+//    an out-of-bounds access becomes SIGSEGV, reported with the faulting
+//    kernel, block and thread.
+#include <hip/hip_runtime.h>
+#include <sched.h>
+#include <signal.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <sys/mman.h>
+#include <time.h>
+#include <ucontext.h>
+#include <execinfo.h>
+#include <unistd.h>
+
+#include <atomic>
+#include <chrono>
+#include <map>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "fs_params.h"
+
+namespace emu {
+
+enum State { RUNNABLE, AT_BARRIER, AT_WAVEOP, DONE };
+enum WaveKind { WK_BALLOT, WK_ALL, WK_SHFL_UP, WK_FIRSTLANE, WK_BARRIER };
+
+struct Fiber {
+    ucontext_t ctx;
+    char* stack = nullptr;
+    State state = RUNNABLE;
+    bool sleeping = false;
+    int pred = 0;
+    int wkind = 0;
+    uint64_t wval = 0, warg = 0, wres = 0;
+};
+
+static size_t stack_bytes() {
+    const char* e = getenv("EMU_STACK_KB");
+    return (size_t)(e ? atoi(e) : 1024) * 1024;
+}
+
+struct Block {
+    uint64_t magic = 0xB10C0B10C0ull;
+    int nthreads = 0;
+    std::vector<Fiber> f;
+    ucontext_t sched;
+    int cur = -1;
+    emu_dim3 bidx{}, bdim{}, gdim{};
+    void (*entry)(void**) = nullptr;
+    void** params = nullptr;
+    int barrier_result = 0;
+};
+
+thread_local Block* B = nullptr;
+static const char* g_kernel = "";
+
+emu_dim3 thread_idx() { return emu_dim3{(uint32_t)B->cur, 0, 0}; }
+emu_dim3 block_idx() { return B->bidx; }
+emu_dim3 block_dim() { return B->bdim; }
+emu_dim3 grid_dim() { return B->gdim; }
+unsigned lane() { return (unsigned)B->cur & 63u; }
+
+[[noreturn]] static void die(const char* why);
+
+static void check_block() {
+    if (!B || B->magic != 0xB10C0B10C0ull || B->cur < 0 || B->cur >= B->nthreads) die("emulator state corrupted");
+}
+
+static void yield_to_sched() {
+    check_block();
+    swapcontext(&B->f[B->cur].ctx, &B->sched);
+    check_block();
+}
+
+void syncthreads() {
+    check_block();
+    Fiber& me = B->f[B->cur];
+    me.state = AT_BARRIER;
+    me.pred = 0;
+    yield_to_sched();
+}
+
+int syncthreads_or(int p) {
+    Fiber& me = B->f[B->cur];
+    me.state = AT_BARRIER;
+    me.pred = p != 0;
+    yield_to_sched();
+    return B->barrier_result;
+}
+
+static uint64_t wave_op(int kind, uint64_t val, uint64_t arg) {
+    Fiber& me = B->f[B->cur];
+    me.state = AT_WAVEOP;
+    me.wkind = kind;
+    me.wval = val;
+    me.warg = arg;
+    yield_to_sched();
+    return me.wres;
+}
+
+uint64_t ballot(int p) { return wave_op(WK_BALLOT, p != 0, 0); }
+int all(int p) { return (int)wave_op(WK_ALL, p != 0, 0); }
+uint32_t shfl_up(uint32_t v, unsigned off) { return (uint32_t)wave_op(WK_SHFL_UP, v, off); }
+uint32_t readfirstlane(uint32_t v) { return (uint32_t)wave_op(WK_FIRSTLANE, v, 0); }
+// Lockstep point: lanes of a wave run one after another between wave
+// operations here, while on the GPU they execute each instruction together;
+// the kernels mark the places where that matters with a wave barrier.
+void wave_barrier() { (void)wave_op(WK_BARRIER, 0, 0); }
+
+void sleep_hint() {
+    Fiber& me = B->f[B->cur];
+    me.sleeping = true;
+    yield_to_sched();
+}
+
+static void fiber_main() {
+    B->entry(B->params);
+    B->f[B->cur].state = DONE;
+    swapcontext(&B->f[B->cur].ctx, &B->sched);
+}
+
+[[noreturn]] static void die(const char* why) {
+    fprintf(stderr, "hip_emu: %s (kernel %s, B=%p)\n", why, g_kernel, (void*)B);
+    fflush(stderr);
+    abort();
+}
+
+static bool resolve_wave(int w) {
+    Block& b = *B;
+    const int lo = w * 64, hi = std::min(b.nthreads, lo + 64);
+    int waiting = 0, kind = -1;
+    for (int i = lo; i < hi; ++i) {
+        if (b.f[i].state == RUNNABLE) return false;     // a lane may still arrive
+        if (b.f[i].state == AT_WAVEOP) {
+            if (kind >= 0 && kind != b.f[i].wkind) die("divergent wave operations in one wave");
+            kind = b.f[i].wkind;
+            ++waiting;
+        }
+    }
+    if (!waiting) return false;
+    uint64_t mask = 0;
+    int first = -1;
+    bool allp = true;
+    for (int i = lo; i < hi; ++i)
+        if (b.f[i].state == AT_WAVEOP) {
+            if (first < 0) first = i;
+            if (b.f[i].wval) mask |= 1ull << (i - lo);
+            allp = allp && b.f[i].wval;
+        }
+    for (int i = lo; i < hi; ++i) {
+        Fiber& f = b.f[i];
+        if (f.state != AT_WAVEOP) continue;
+        switch (kind) {
+            case WK_BALLOT: f.wres = mask; break;
+            case WK_ALL: f.wres = allp; break;
+            case WK_FIRSTLANE: f.wres = b.f[first].wval; break;
+            case WK_BARRIER: f.wres = 0; break;
+            case WK_SHFL_UP: {
+                const int src = (i - lo) - (int)f.warg;
+                f.wres = (src >= 0 && b.f[lo + src].state == AT_WAVEOP) ? b.f[lo + src].wval : f.wval;
+                break;
+            }
+        }
+    }
+    for (int i = lo; i < hi; ++i)
+        if (b.f[i].state == AT_WAVEOP) b.f[i].state = RUNNABLE;
+    return true;
+}
+
+static void run_block(uint32_t bid, uint32_t grid, uint32_t nthreads, void (*entry)(void**), void** params) {
+    Block b;
+    b.nthreads = (int)nthreads;
+    b.f.resize(nthreads);
+    b.bidx = {bid, 0, 0};
+    b.bdim = {nthreads, 1, 1};
+    b.gdim = {grid, 1, 1};
+    b.entry = entry;
+    b.params = params;
+    B = &b;
+    for (uint32_t i = 0; i < nthreads; ++i) {
+        Fiber& f = b.f[i];
+        f.stack = (char*)malloc(stack_bytes());
+        getcontext(&f.ctx);
+        f.ctx.uc_stack.ss_sp = f.stack;
+        f.ctx.uc_stack.ss_size = stack_bytes();
+        f.ctx.uc_link = nullptr;
+        makecontext(&f.ctx, fiber_main, 0);
+    }
+    for (;;) {
+        bool ran = false, awake = false;
+        for (int i = 0; i < b.nthreads; ++i) {
+            if (b.f[i].state != RUNNABLE) continue;
+            if (!b.f[i].sleeping) awake = true;
+            b.f[i].sleeping = false;
+            b.cur = i;
+            swapcontext(&b.sched, &b.f[i].ctx);
+            ran = true;
+        }
+        b.cur = -1;
+        bool resolved = false;
+        for (int w = 0; w * 64 < b.nthreads; ++w) resolved |= resolve_wave(w);
+        int live = 0, at_bar = 0, orv = 0;
+        for (auto& f : b.f) {
+            if (f.state == DONE) continue;
+            ++live;
+            if (f.state == AT_BARRIER) { ++at_bar; orv |= f.pred; }
+        }
+        if (live == 0) break;
+        if (at_bar == live) {
+            b.barrier_result = orv;
+            for (auto& f : b.f)
+                if (f.state == AT_BARRIER) f.state = RUNNABLE;
+            resolved = true;
+        }
+        if (!ran && !resolved) die("deadlock: every live thread waits and nothing can resolve");
+        if (ran && !awake && !resolved) sched_yield();   // the whole block is spin-waiting
+    }
+    for (auto& f : b.f) free(f.stack);
+    B = nullptr;
+}
+
+static int workers() {
+    const char* e = getenv("EMU_WORKERS");
+    int w = e ? atoi(e) : 4;
+    return w > 0 ? w : 1;
+}
+
+void launch(const char* name, void (*entry)(void**), uint32_t grid, uint32_t block, void** params) {
+    g_kernel = name;
+    if (getenv("EMU_TRACE")) fprintf(stderr, "hip_emu: launch %s grid=%u block=%u\n", name, grid, block);
+    std::atomic<uint32_t> next{0};
+    auto worker = [&]() {
+        if (!getenv("EMU_NO_SEGV_HANDLER")) {
+            stack_t ss;                   // the signal handler's stack; kept for the process
+            ss.ss_size = 1 << 16;
+            ss.ss_sp = malloc(ss.ss_size);
+            ss.ss_flags = 0;
+            sigaltstack(&ss, nullptr);
+        }
+        for (;;) {
+            const uint32_t b = next.fetch_add(1);
+            if (b >= grid) break;
+            run_block(b, grid, block, entry, params);
+        }
+    };
+    std::vector<std::thread> pool;
+    const int nw = std::min<int>(workers(), (int)grid);
+    for (int i = 0; i < nw; ++i) pool.emplace_back(worker);
+    for (auto& t : pool) t.join();
+}
+
+}  // namespace emu
+
+// ---------------------------------------------------------------------------
+// kernels of radix_kernels.hip (compiled into the same library) and their
+// argument unpacking
+// ---------------------------------------------------------------------------
+extern "C" {
+void fs_upsweep_k32(FsArgs);
+void fs_upsweep_k64(FsArgs);
+void fs_plan(FsArgs);
+void fs_onesweep_k32(FsArgs, uint32_t);
+void fs_onesweep_k32_v(FsArgs, uint32_t);
+void fs_onesweep_k64(FsArgs, uint32_t);
+void fs_onesweep_k64_v(FsArgs, uint32_t);
+void fs_finish(FsArgs);
+void fs_iota(uint32_t*, uint64_t);
+extern uint32_t fs_kernel_tile_keys[4];
+extern uint32_t fs_kernel_block_threads[4];
+}
+
+struct emu_function {
+    const char* name;
+    void (*entry)(void**);
+};
+
+#define A0 (*(FsArgs*)p[0])
+#define D1 (*(uint32_t*)p[1])
+static emu_function g_funcs[] = {
+    {"fs_upsweep_k32", [](void** p) { fs_upsweep_k32(A0); }},
+    {"fs_upsweep_k64", [](void** p) { fs_upsweep_k64(A0); }},
+    {"fs_plan", [](void** p) { fs_plan(A0); }},
+    {"fs_onesweep_k32", [](void** p) { fs_onesweep_k32(A0, D1); }},
+    {"fs_onesweep_k32_v", [](void** p) { fs_onesweep_k32_v(A0, D1); }},
+    {"fs_onesweep_k64", [](void** p) { fs_onesweep_k64(A0, D1); }},
+    {"fs_onesweep_k64_v", [](void** p) { fs_onesweep_k64_v(A0, D1); }},
+    {"fs_finish", [](void** p) { fs_finish(A0); }},
+    {"fs_iota", [](void** p) { fs_iota(*(uint32_t**)p[0], *(uint64_t*)p[1]); }},
+};
+
+struct emu_module { int dummy; };
+struct emu_stream { int dummy; };
+struct emu_event { std::chrono::steady_clock::time_point t; };
+
+// ---------------------------------------------------------------------------
+// guard-page device memory
+// ---------------------------------------------------------------------------
+namespace {
+std::mutex g_mu;
+std::map<void*, std::pair<char*, size_t>> g_allocs;   // user ptr -> (mapping, length)
+const size_t kPage = 4096;
+
+void on_segv(int, siginfo_t* si, void*) {
+    char msg[256];
+    snprintf(msg, sizeof msg, "hip_emu: device memory fault at %p (kernel %s, block %d, thread %d)\n",
+             si->si_addr, emu::g_kernel, emu::B ? (int)emu::B->bidx.x : -1, emu::B ? emu::B->cur : -1);
+    if (write(2, msg, strlen(msg)) < 0) {}
+    void* frames[64];
+    const int nf = backtrace(frames, 64);
+    backtrace_symbols_fd(frames, nf, 2);
+    _exit(86);
+}
+
+struct SegvInstaller {
+    SegvInstaller() {
+        if (getenv("EMU_NO_SEGV_HANDLER")) return;
+        struct sigaction sa;
+        memset(&sa, 0, sizeof sa);
+        sa.sa_sigaction = on_segv;
+        sa.sa_flags = SA_SIGINFO | SA_ONSTACK;
+        sigaction(SIGSEGV, &sa, nullptr);
+    }
+} g_segv;
+}  // namespace
+
+hipError_t hipMalloc(void** p, size_t n) {
+    const size_t body = (n + kPage - 1) / kPage * kPage;
+    const size_t len = body + 2 * kPage;
+    char* m = (char*)mmap(nullptr, len, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
+    if (m == MAP_FAILED) return hipErrorOutOfMemory;
+    mprotect(m, kPage, PROT_NONE);
+    mprotect(m + kPage + body, kPage, PROT_NONE);
+    const size_t n16 = (n + 15) / 16 * 16;
+    char* user = m + kPage + body - n16;       // ends on the trailing guard page (16-byte aligned)
+    std::lock_guard<std::mutex> g(g_mu);
+    g_allocs[user] = {m, len};
+    *p = user;
+    return hipSuccess;
+}
+
+hipError_t hipFree(void* p) {
+    if (!p) return hipSuccess;
+    std::lock_guard<std::mutex> g(g_mu);
+    auto it = g_allocs.find(p);
+    if (it == g_allocs.end()) return hipErrorInvalidValue;
+    munmap(it->second.first, it->second.second);
+    g_allocs.erase(it);
+    return hipSuccess;
+}
+
+hipError_t hipHostMalloc(void** p, size_t n, unsigned) { return hipMalloc(p, n); }
+hipError_t hipHostFree(void* p) { return hipFree(p); }
+hipError_t hipMemset(void* p, int v, size_t n) { memset(p, v, n); return hipSuccess; }
+hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind) { memmove(d, s, n); return hipSuccess; }
+hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t) { return hipMemcpy(d, s, n, k); }
+hipError_t hipMemcpyDtoH(void* d, hipDeviceptr_t s, size_t n) { memcpy(d, s, n); return hipSuccess; }
+
+hipError_t hipGetDeviceCount(int* c) { *c = 1; return hipSuccess; }
+hipError_t hipSetDevice(int d) { return d == 0 ? hipSuccess : hipErrorInvalidValue; }
+hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
+    const char* e = getenv("EMU_CUS");
+    *v = e ? atoi(e) : 2;
+    return hipSuccess;
+}
+hipError_t hipGetLastError(void) { return hipSuccess; }
+const char* hipGetErrorString(hipError_t e) { return e == hipSuccess ? "success" : "emulated HIP error"; }
+hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned) { *s = new emu_stream(); return hipSuccess; }
+hipError_t hipStreamDestroy(hipStream_t s) { delete s; return hipSuccess; }
+hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+hipError_t hipDeviceSynchronize(void) { return hipSuccess; }
+
+hipError_t hipModuleLoad(hipModule_t* m, const char*) { *m = new emu_module(); return hipSuccess; }
+hipError_t hipModuleUnload(hipModule_t m) { delete m; return hipSuccess; }
+hipError_t hipModuleGetFunction(hipFunction_t* f, hipModule_t, const char* name) {
+    for (auto& e : g_funcs)
+        if (!strcmp(e.name, name)) { *f = &e; return hipSuccess; }
+    return hipErrorNotFound;
+}
+hipError_t hipModuleGetGlobal(hipDeviceptr_t* p, size_t* sz, hipModule_t, const char* name) {
+    if (!strcmp(name, "fs_kernel_tile_keys")) { *p = fs_kernel_tile_keys; *sz = sizeof fs_kernel_tile_keys; return hipSuccess; }
+    if (!strcmp(name, "fs_kernel_block_threads")) { *p = fs_kernel_block_threads; *sz = sizeof fs_kernel_block_threads; return hipSuccess; }
+    return hipErrorNotFound;
+}
+hipError_t hipModuleLaunchKernel(hipFunction_t f, unsigned gx, unsigned, unsigned, unsigned bx, unsigned,
+                                 unsigned, unsigned, hipStream_t, void** params, void**) {
+    emu::launch(f->name, f->entry, gx, bx, params);
+    return hipSuccess;
+}
+hipError_t hipEventCreate(hipEvent_t* e) { *e = new emu_event(); return hipSuccess; }
+hipError_t hipEventDestroy(hipEvent_t e) { delete e; return hipSuccess; }
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t) { e->t = std::chrono::steady_clock::now(); return hipSuccess; }
+hipError_t hipEventElapsedTime(float* ms, hipEvent_t a, hipEvent_t b) {
+    *ms = std::chrono::duration<float, std::milli>(b->t - a->t).count();
+    return hipSuccess;
+}

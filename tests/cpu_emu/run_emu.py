@@ -1,0 +1,82 @@
+"""Runs the product's C ABI, built for the CPU emulator, against the oracle
+(TEST INFRASTRUCTURE ONLY).  Usage: python run_emu.py <small|prod> <case> ...
+
+Executed in a subprocess by tests/test_cpu_emulation.py so that an emulated
+device memory fault (the guard pages turn it into SIGSEGV -> exit code 86)
+or an emulator deadlock cannot take the test runner down.  The forge_sort
+package is pointed at the emulation library only inside this process.
+"""
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path[:0] = [os.path.join(ROOT, "gpu-forge_amd"), os.path.join(ROOT, "oracle")]
+
+import numpy as np  # noqa: E402
+
+import oracle  # noqa: E402
+import forge_sort  # noqa: E402
+from forge_sort import _build  # noqa: E402
+
+BITS = {"u32": np.uint32, "i32": np.uint32, "f32": np.uint32,
+        "u64": np.uint64, "i64": np.uint64, "f64": np.uint64}
+
+
+def use_emulator(flavor):
+    lib = os.path.join(HERE, "_build", f"libforge_sort_emu_{flavor}.so")
+    _build.SO = lib
+    _build.HSACO = lib          # existence check only; the emulator ignores the path
+    forge_sort._lib = None
+
+
+def keys_for(kind, n, dist, seed):
+    g = np.random.Generator(np.random.PCG64(seed))
+    wide = BITS[kind] == np.uint64
+    if dist == "uniform":
+        b = g.integers(0, 1 << (64 if wide else 32), size=n, dtype=BITS[kind], endpoint=False)
+    elif dist == "few":
+        b = g.choice(g.integers(0, 1 << (64 if wide else 32), size=5, dtype=BITS[kind], endpoint=False), size=n)
+    elif dist == "same":
+        b = np.full(n, 7, dtype=BITS[kind])
+    elif dist == "low12":
+        b = g.integers(0, 1 << 12, size=n, dtype=BITS[kind])
+    else:
+        raise ValueError(dist)
+    return b.view(oracle.NP_DTYPES[kind])
+
+
+def check(sorter, op, kind, n, dist, seed):
+    keys = keys_for(kind, n, dist, seed)
+    if op == "sort":
+        got = keys.copy()
+        getattr(sorter, f"sort_{kind}")(got)
+        ok = np.array_equal(got.view(BITS[kind]), oracle.sort(kind, keys).view(BITS[kind]))
+    elif op == "argsort":
+        ok = np.array_equal(getattr(sorter, f"argsort_{kind}")(keys), oracle.argsort(kind, keys))
+    else:
+        vals = np.arange(n, dtype=np.uint32)[::-1].copy()
+        ek, ev = oracle.sort_pairs(kind, keys, vals)
+        gk, gv = keys.copy(), vals.copy()
+        getattr(sorter, f"sort_pairs_{kind}")(gk, gv)
+        ok = np.array_equal(gk.view(BITS[kind]), ek.view(BITS[kind])) and np.array_equal(gv, ev)
+    passes, mask = sorter.last_pass_info()
+    print(f"{'PASS' if ok else 'FAIL'} {op} {kind} n={n} {dist} passes={passes} mask={mask:#x}", flush=True)
+    return ok
+
+
+def main():
+    flavor = sys.argv[1]
+    use_emulator(flavor)
+    sorter = forge_sort.GpuSorter.new()
+    print("tiles", sorter.tile_config(), flush=True)
+    ok = True
+    for spec in sys.argv[2:]:
+        op, kind, n, dist, seed = spec.split(":")
+        ok &= check(sorter, op, kind, int(n), dist, int(seed))
+    sorter.close()
+    sys.exit(0 if ok else 1)
+
+
+if __name__ == "__main__":
+    main()

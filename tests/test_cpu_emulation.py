@@ -1,0 +1,70 @@
+"""The product's kernels and host runtime, compiled for the CPU emulator in
+tests/cpu_emu (fibers per GPU thread, guard-paged device allocations), checked
+against the oracle.
+
+Each case list runs in a child process (tests/cpu_emu/run_emu.py): an emulated
+out-of-bounds device access ends that process with SIGSEGV (exit 86 after the
+emulator's report), and a deadlocked emulation is cut off by the timeout,
+without taking the test runner down.  Two builds are covered: "small" (tiny
+tiles, so a few thousand keys span many tiles, portions of the look-back chain
+and the tail paths) and "prod" (the tile geometry the gfx950 build uses).
+"""
+import os
+import shutil
+import subprocess
+import sys
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+EMU = os.path.join(HERE, "cpu_emu")
+
+pytestmark = pytest.mark.skipif(shutil.which("g++") is None or shutil.which("make") is None,
+                                reason="needs g++ and make")
+
+
+@pytest.fixture(scope="module")
+def emulator():
+    r = subprocess.run(["make", "-C", EMU, "-j2"], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+    return EMU
+
+
+def run_cases(flavor, cases, timeout=300):
+    r = subprocess.run([sys.executable, os.path.join(EMU, "run_emu.py"), flavor, *cases],
+                       capture_output=True, text=True, timeout=timeout)
+    lines = [ln for ln in r.stdout.splitlines() if ln.startswith(("PASS", "FAIL"))]
+    assert r.returncode == 0 and len(lines) == len(cases) and all(ln.startswith("PASS") for ln in lines), \
+        f"exit {r.returncode}\n{r.stdout}\n{r.stderr[-4000:]}"
+    return lines
+
+
+SMALL_CASES = [
+    # every op x key type, sizes spanning many small tiles
+    "sort:u32:5000:uniform:1", "sort:i32:4099:uniform:2", "sort:f32:6001:uniform:3",
+    "sort:u64:3000:uniform:4", "sort:i64:2049:uniform:5", "sort:f64:3001:uniform:6",
+    "argsort:u32:3000:few:7", "argsort:f32:9000:few:8", "argsort:i64:2500:uniform:9",
+    "pairs:u32:8000:uniform:10", "pairs:i32:3333:few:11", "pairs:f64:2500:uniform:12",
+    "pairs:u64:1999:few:13",
+    # constant digits skipped on the device (2 live passes, 0 live passes)
+    "sort:u32:7000:low12:14", "sort:i64:4000:low12:15", "pairs:f32:6000:low12:16",
+    "argsort:u32:3000:same:17", "sort:u64:2000:same:18",
+    # trivial and ragged lengths (vector path off for odd n)
+    "sort:u32:0:uniform:19", "sort:u32:1:uniform:20", "sort:u32:2:uniform:21",
+    "sort:u32:63:uniform:22", "sort:u32:65:uniform:23", "pairs:u64:3:uniform:24",
+    "argsort:f64:1025:uniform:25",
+]
+
+PROD_CASES = [
+    "sort:u32:40000:uniform:1", "sort:u32:12289:uniform:2", "argsort:f32:30000:few:3",
+    "pairs:u64:20000:uniform:4", "sort:i64:20000:low12:6", "pairs:u32:25000:few:7",
+    "sort:f64:9000:uniform:8", "argsort:i32:13000:uniform:9",
+]
+
+
+def test_emulated_small_tiles(emulator):
+    run_cases("small", SMALL_CASES)
+
+
+def test_emulated_production_tiles(emulator):
+    run_cases("prod", PROD_CASES)
