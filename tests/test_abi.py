@@ -49,9 +49,10 @@ def test_status_strings_match_sort_error_display():
 
 def test_no_device_is_reported_not_raised_as_crash():
     """Without a GPU (this container), construction fails with DeviceNotFound."""
-    import torch
-    if torch.cuda.is_available():
-        pytest.skip("a GPU is present")
     from forge_sort import DeviceNotFound, GpuSorter
-    with pytest.raises(DeviceNotFound):
-        GpuSorter.new()
+    try:
+        s = GpuSorter.new()
+    except DeviceNotFound:
+        return
+    s.close()
+    pytest.skip("a GPU is present")
