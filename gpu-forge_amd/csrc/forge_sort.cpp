@@ -80,21 +80,27 @@ struct fs_sorter {
 // helpers
 // ---------------------------------------------------------------------------
 
+// Message of the last failed construction on this thread (there is no sorter
+// to hold it); fs_last_error(NULL) returns it.
+static thread_local std::string g_create_err;
+
+static std::string display(fs_status st, const char* detail) {
+    // Display strings of SortError (lib.rs:94-104)
+    switch (st) {
+        case FS_ERR_DEVICE_NOT_FOUND: return "no HIP GPU device found";
+        case FS_ERR_SHADER_COMPILATION: return std::string("shader compilation failed: ") + detail;
+        case FS_ERR_GPU_EXECUTION: return std::string("GPU execution failed: ") + detail;
+        default: return detail;
+    }
+}
+
 static fs_status set_err(fs_sorter* s, fs_status st, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(buf, sizeof buf, fmt, ap);
     va_end(ap);
-    if (s) {
-        // Display strings of SortError (lib.rs:94-104)
-        switch (st) {
-            case FS_ERR_DEVICE_NOT_FOUND: s->err = "no HIP GPU device found"; break;
-            case FS_ERR_SHADER_COMPILATION: s->err = std::string("shader compilation failed: ") + buf; break;
-            case FS_ERR_GPU_EXECUTION: s->err = std::string("GPU execution failed: ") + buf; break;
-            default: s->err = buf; break;
-        }
-    }
+    if (s) s->err = display(st, buf);
     return st;
 }
 
@@ -344,24 +350,30 @@ fs_status fs_tile_config(const fs_sorter* s, uint32_t keys_per_tile[4]) {
     return FS_OK;
 }
 
-const char* fs_last_error(const fs_sorter* s) { return s ? s->err.c_str() : "null sorter"; }
+const char* fs_last_error(const fs_sorter* s) { return s ? s->err.c_str() : g_create_err.c_str(); }
+
+// Frees a partly built sorter and records why construction failed.
+static fs_status create_failed(fs_sorter* s, fs_status st, const std::string& detail) {
+    g_create_err = display(st, detail.c_str());
+    if (s) fs_sorter_free(s);
+    return st;
+}
 
 static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** out) {
-    if (!out) return FS_ERR_INVALID_ARGUMENT;
+    if (!out) return create_failed(nullptr, FS_ERR_INVALID_ARGUMENT, "null output pointer");
     *out = nullptr;
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0 || device < 0 || device >= count) {
         (void)hipGetLastError();
-        return FS_ERR_DEVICE_NOT_FOUND;
+        return create_failed(nullptr, FS_ERR_DEVICE_NOT_FOUND, "");
     }
     fs_sorter* s = new (std::nothrow) fs_sorter();
-    if (!s) return FS_ERR_OUT_OF_MEMORY;
+    if (!s) return create_failed(nullptr, FS_ERR_OUT_OF_MEMORY, "host allocation of the sorter");
     s->device = device;
-    fs_status r = FS_OK;
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) {
         delete s;
-        return FS_ERR_DEVICE_NOT_FOUND;
+        return create_failed(nullptr, FS_ERR_DEVICE_NOT_FOUND, "");
     }
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
@@ -370,7 +382,7 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
         e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
         if (e != hipSuccess) {
             delete s;
-            return FS_ERR_GPU_EXECUTION;
+            return create_failed(nullptr, FS_ERR_GPU_EXECUTION, std::string("hipStreamCreate: ") + hipGetErrorString(e));
         }
         s->own_stream = true;
     } else {
@@ -380,18 +392,14 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
 
     const std::string path = code_object_path();
     e = hipModuleLoad(&s->module, path.c_str());
-    if (e != hipSuccess) {
-        r = set_err(s, FS_ERR_SHADER_COMPILATION, "hipModuleLoad(%s): %s", path.c_str(),
-                    hipGetErrorString(e));
-        fs_sorter_free(s);
-        return r;
-    }
+    if (e != hipSuccess)
+        return create_failed(s, FS_ERR_SHADER_COMPILATION,
+                             "hipModuleLoad(" + path + "): " + hipGetErrorString(e));
     for (int k = 0; k < K_COUNT; ++k) {
         e = hipModuleGetFunction(&s->fn[k], s->module, kKernelNames[k]);
-        if (e != hipSuccess) {
-            fs_sorter_free(s);
-            return FS_ERR_SHADER_COMPILATION;
-        }
+        if (e != hipSuccess)
+            return create_failed(s, FS_ERR_SHADER_COMPILATION, std::string("kernel ") + kKernelNames[k] +
+                                 " missing from the code object");
     }
     {
         // tile geometry compiled into the code object
@@ -400,34 +408,27 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
         if (hipModuleGetGlobal(&gp, &gsz, s->module, "fs_kernel_tile_keys") != hipSuccess || gsz != 16 ||
             hipModuleGetGlobal(&bp, &bsz, s->module, "fs_kernel_block_threads") != hipSuccess || bsz != 16 ||
             hipMemcpyDtoH(s->tile, gp, 16) != hipSuccess || hipMemcpyDtoH(s->block, bp, 16) != hipSuccess) {
-            r = set_err(s, FS_ERR_SHADER_COMPILATION, "code object lacks fs_kernel_tile_keys/fs_kernel_block_threads");
-            fs_sorter_free(s);
-            return r;
+            return create_failed(s, FS_ERR_SHADER_COMPILATION,
+                                 "code object lacks fs_kernel_tile_keys/fs_kernel_block_threads");
         }
         for (int i = 0; i < 4; ++i)
-            if (s->tile[i] == 0 || s->block[i] < FS_RADIX) {
-                fs_sorter_free(s);
-                return FS_ERR_SHADER_COMPILATION;
-            }
+            if (s->tile[i] == 0 || s->block[i] < FS_RADIX)
+                return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object has an invalid tile geometry");
     }
     const size_t tab = (size_t)FS_MAX_PORTIONS * FS_MAX_DIGITS * FS_RADIX * 4;
     if (hipMalloc(&s->hist, tab) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||
         hipMalloc(&s->tile_ctr, FS_MAX_DIGITS * 4) != hipSuccess ||
         hipMalloc(&s->plan, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc(&s->stats, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
-        hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
-        fs_sorter_free(s);
-        return FS_ERR_OUT_OF_MEMORY;
-    }
+        hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
+        return create_failed(s, FS_ERR_OUT_OF_MEMORY, "device tables of the sorter");
     *s->status = 0;
     // The histogram table must start at zero; fs_plan re-zeroes it after every sort.
     if (hipMemset(s->hist, 0, tab) != hipSuccess || hipMemset(s->tile_ctr, 0, FS_MAX_DIGITS * 4) != hipSuccess ||
         hipMemset(s->stats, 0, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipMemset(s->plan, 0, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
-        hipDeviceSynchronize() != hipSuccess) {
-        fs_sorter_free(s);
-        return FS_ERR_GPU_EXECUTION;
-    }
+        hipDeviceSynchronize() != hipSuccess)
+        return create_failed(s, FS_ERR_GPU_EXECUTION, "clearing the device tables");
     *out = s;
     return FS_OK;
 }

@@ -262,7 +262,7 @@ class GpuSorter:
         else:
             st = L.fs_sorter_new(device, ctypes.byref(h))
         if st != FS_OK:
-            msg = L.fs_status_str(st).decode()
+            msg = L.fs_last_error(None).decode() or L.fs_status_str(st).decode()
             raise _ERRORS.get(st, SortError)(msg)
         self._h = h
         self.device = device

@@ -74,7 +74,9 @@ fs_status fs_sorter_with_context(int device, void *hip_stream, fs_sorter **out);
 /* Drop for GpuSorter: frees scratch, unloads the module, destroys an owned stream. */
 void fs_sorter_free(fs_sorter *s);
 
-/* The message of the last failing call (SortError's Display text, lib.rs:94-104). */
+/* The message of the last failing call (SortError's Display text, lib.rs:94-104).
+ * With s == NULL: why the last fs_sorter_new / fs_sorter_with_context on this
+ * thread failed. */
 const char *fs_last_error(const fs_sorter *s);
 
 /* Display text of a status code. */

@@ -52,7 +52,8 @@ def test_no_device_is_reported_not_raised_as_crash():
     from forge_sort import DeviceNotFound, GpuSorter
     try:
         s = GpuSorter.new()
-    except DeviceNotFound:
+    except DeviceNotFound as e:
+        assert str(e) == "no HIP GPU device found"     # SortError::DeviceNotFound's Display
         return
     s.close()
     pytest.skip("a GPU is present")
