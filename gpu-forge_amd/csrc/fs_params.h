@@ -14,33 +14,28 @@
 // per kernel variant.  The host reads the tile sizes from the code object
 // (fs_kernel_tile_keys / fs_kernel_block_threads), so they are only defined here.
 #ifndef FS_K32_BLOCK
-#define FS_K32_BLOCK 512
+#define FS_K32_BLOCK 768
 #endif
 #ifndef FS_K32_ITEMS
-#define FS_K32_ITEMS 24
+#define FS_K32_ITEMS 16
 #endif
 #ifndef FS_K32V_BLOCK
-#define FS_K32V_BLOCK 256
+#define FS_K32V_BLOCK 768
 #endif
 #ifndef FS_K32V_ITEMS
-#define FS_K32V_ITEMS 16
+#define FS_K32V_ITEMS 12
 #endif
 #ifndef FS_K64_BLOCK
-#define FS_K64_BLOCK 256
+#define FS_K64_BLOCK 768
 #endif
 #ifndef FS_K64_ITEMS
-#define FS_K64_ITEMS 16
+#define FS_K64_ITEMS 8
 #endif
 #ifndef FS_K64V_BLOCK
-#define FS_K64V_BLOCK 256
+#define FS_K64V_BLOCK 768
 #endif
 #ifndef FS_K64V_ITEMS
-#define FS_K64V_ITEMS 12
-#endif
-// Ranking inside a wave: 0 = ballot match (8 ballots per key),
-// 1 = LDS atomic-OR lane masks.
-#ifndef FS_RANK_MODE
-#define FS_RANK_MODE 0
+#define FS_K64V_ITEMS 8
 #endif
 // index into fs_kernel_tile_keys
 #define FS_VAR_K32 0

@@ -144,6 +144,26 @@ def test_sort_sizes(sorter, kind, n):
     check_sort(sorter, kind, make_keys(kind, n, "uniform", seed=n))
 
 
+TILE_VARIANT = {("sort", False): "k32", ("sort", True): "k64", ("argsort", False): "k32_v",
+                ("argsort", True): "k64_v", ("pairs", False): "k32_v", ("pairs", True): "k64_v"}
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("op", ["sort", "argsort", "pairs"])
+def test_tile_boundaries(sorter, kind, op):
+    """Sizes at the edges of the kernel's own tile (read from the code object):
+    one tile less one key, one tile, one tile plus one, two tiles plus one."""
+    tile = sorter.tile_config()[TILE_VARIANT[(op, BITS[kind] == np.uint64)]]
+    for n in (tile - 1, tile, tile + 1, 2 * tile + 1):
+        keys = make_keys(kind, n, "few" if op == "argsort" else "uniform", seed=300 + n)
+        if op == "sort":
+            check_sort(sorter, kind, keys)
+        elif op == "argsort":
+            check_argsort(sorter, kind, keys)
+        else:
+            check_pairs(sorter, kind, keys, np.arange(n, dtype=np.uint32)[::-1].copy())
+
+
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("dist", ["zeros", "same", "sorted", "reverse", "few", "lowbits"])
 def test_sort_distributions(sorter, kind, dist):
