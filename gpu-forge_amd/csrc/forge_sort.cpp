@@ -259,8 +259,10 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         if ((r = ensure(s, s->s1v, n * 4)) != FS_OK) return r;
         if (op == FS_OP_PAIRS && (r = ensure(s, s->s2v, n * 4)) != FS_OK) return r;
     }
-    if ((r = ensure(s, s->lb0, (size_t)num_tiles * FS_RADIX * 4)) != FS_OK) return r;
-    if ((r = ensure(s, s->lb1, (size_t)num_tiles * FS_RADIX * 4)) != FS_OK) return r;
+    // look-back arrays: tile entries, then one group entry per FS_LB_GROUP tiles
+    const size_t lb_bytes = ((size_t)num_tiles + (num_tiles + FS_LB_GROUP - 1) / FS_LB_GROUP) * FS_RADIX * 4;
+    if ((r = ensure(s, s->lb0, lb_bytes)) != FS_OK) return r;
+    if ((r = ensure(s, s->lb1, lb_bytes)) != FS_OK) return r;
 
     FsArgs a;
     memset(&a, 0, sizeof a);
@@ -273,6 +275,8 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     // portions: the largest power-of-two tile count holding at most 2^30 keys
     uint32_t tpp = 1;
     while ((uint64_t)tpp * 2u * tile <= FS_PORTION_KEYS) tpp <<= 1;
+    if (tpp % FS_LB_GROUP != 0)    // look-back groups must not straddle a chain start
+        return set_err(s, FS_ERR_INVALID_ARGUMENT, "tile of %u keys too large for look-back groups", tile);
     a.tiles_per_portion = tpp;
     a.tile = tile;
     a.vec_ok = ((uintptr_t)keys % 16 == 0) ? 1u : 0u;

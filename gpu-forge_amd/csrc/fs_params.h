@@ -65,10 +65,23 @@
 #define FS_EARLY_AGG 2
 #endif
 
-// Predecessor entries read per look-back round trip.
+// Predecessor tile entries read per look-back round trip.
 #ifndef FS_LB_WINDOW
 #define FS_LB_WINDOW 4
 #endif
+// Second look-back level: FS_LB_GROUP consecutive tiles (a power of two that
+// divides tiles_per_portion) share a group entry per digit holding
+// (tiles added << FS_LB_GCOUNT_SHIFT) | sum of their counts; FS_LB_GWIN groups
+// are read per round trip.  FS_LB_GROUP * tile keys < 2^24 keeps the sum in
+// its field.
+#ifndef FS_LB_GROUP
+#define FS_LB_GROUP 16
+#endif
+#ifndef FS_LB_GWIN
+#define FS_LB_GWIN 4
+#endif
+#define FS_LB_GCOUNT_SHIFT 24
+#define FS_LB_GSUM 0x00FFFFFFu
 
 // Bounded spin of a look-back wait (iterations of s_sleep(1), ~64 clocks each).
 // A predecessor tile that owns a tile id is resident and finishes in

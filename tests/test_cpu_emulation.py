@@ -7,7 +7,8 @@ out-of-bounds device access ends that process with SIGSEGV (exit 86 after the
 emulator's report), and a deadlocked emulation is cut off by the timeout,
 without taking the test runner down.  Two builds are covered: "small" (tiny
 tiles, so a few thousand keys span many tiles, portions of the look-back chain
-and the tail paths) and "prod" (the tile geometry the gfx950 build uses).
+and the tail paths) "prod" (the tile geometry the gfx950 build uses) and "groups" (tiny tiles
+and look-back groups of two tiles, so that look-backs walk whole groups).
 """
 import os
 import shutil
@@ -30,9 +31,10 @@ def emulator():
     return EMU
 
 
-def run_cases(flavor, cases, timeout=300):
+def run_cases(flavor, cases, timeout=300, env=None):
     r = subprocess.run([sys.executable, os.path.join(EMU, "run_emu.py"), flavor, *cases],
-                       capture_output=True, text=True, timeout=timeout)
+                       capture_output=True, text=True, timeout=timeout,
+                       env=dict(os.environ, **(env or {})))
     lines = [ln for ln in r.stdout.splitlines() if ln.startswith(("PASS", "FAIL"))]
     assert r.returncode == 0 and len(lines) == len(cases) and all(ln.startswith("PASS") for ln in lines), \
         f"exit {r.returncode}\n{r.stdout}\n{r.stderr[-4000:]}"
@@ -68,3 +70,13 @@ def test_emulated_small_tiles(emulator):
 
 def test_emulated_production_tiles(emulator):
     run_cases("prod", PROD_CASES)
+
+
+
+def test_emulated_lookback_groups(emulator):
+    """Look-back groups of two tiles, one tile entry per round trip, eight
+    emulated CUs: most look-backs cross several groups, and predecessors are
+    often still unpublished."""
+    run_cases("groups", ["sort:u32:70000:uniform:2", "sort:i64:9000:uniform:3", "argsort:f32:33333:few:4",
+                         "pairs:u64:5000:low12:5", "sort:u32:1025:uniform:6", "pairs:u32:40000:uniform:7"],
+              env={"EMU_CUS": "8"})
