@@ -58,8 +58,8 @@ struct fs_sorter {
     int num_cus = 256;
 
     DevBuf s1k, s2k, s1v, s2v, lb0, lb1, iok, iov;
-    uint32_t* hist = nullptr;       // [FS_MAX_PORTIONS][8][256], zero between sorts
-    uint32_t* binbase = nullptr;    // [FS_MAX_PORTIONS][8][256]
+    uint32_t* hist = nullptr;       // [8][256], zero between sorts
+    uint32_t* binbase = nullptr;    // [8][256]
     uint32_t* tile_ctr = nullptr;   // [8]
     uint32_t* plan = nullptr;       // u32[FS_PLAN_WORDS] device-side schedule
     uint32_t* status = nullptr;     // pinned host word written by kernels on device errors
@@ -259,8 +259,14 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         if ((r = ensure(s, s->s1v, n * 4)) != FS_OK) return r;
         if (op == FS_OP_PAIRS && (r = ensure(s, s->s2v, n * 4)) != FS_OK) return r;
     }
-    // look-back arrays: tile entries, then one group entry per FS_LB_GROUP tiles
-    const size_t lb_bytes = ((size_t)num_tiles + (num_tiles + FS_LB_GROUP - 1) / FS_LB_GROUP) * FS_RADIX * 4;
+    // Look-back arrays: tile entries (64-bit once an inclusive prefix may need
+    // more than 30 bits), then one 32-bit group entry per FS_LB_GROUP tiles.
+    // FS_LB_FORCE_WIDE=1 selects the 64-bit entries for any n (a test switch
+    // for that layout).
+    const char* force_wide = getenv("FS_LB_FORCE_WIDE");
+    const bool wide = n >= FS_LB_WIDE_KEYS || (force_wide && force_wide[0] == '1');
+    const size_t lb_bytes = (size_t)num_tiles * FS_RADIX * (wide ? 8 : 4) +
+                            (size_t)((num_tiles + FS_LB_GROUP - 1) / FS_LB_GROUP) * FS_RADIX * 4;
     if ((r = ensure(s, s->lb0, lb_bytes)) != FS_OK) return r;
     if ((r = ensure(s, s->lb1, lb_bytes)) != FS_OK) return r;
 
@@ -272,12 +278,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.op = op == FS_OP_SORT ? FSK_OP_KEYS : (op == FS_OP_ARGSORT ? FSK_OP_ARGSORT : FSK_OP_PAIRS);
     a.digits = key64(t) ? 8u : 4u;     // one 8-bit digit per key byte
     a.num_tiles = num_tiles;
-    // portions: the largest power-of-two tile count holding at most 2^30 keys
-    uint32_t tpp = 1;
-    while ((uint64_t)tpp * 2u * tile <= FS_PORTION_KEYS) tpp <<= 1;
-    if (tpp % FS_LB_GROUP != 0)    // look-back groups must not straddle a chain start
-        return set_err(s, FS_ERR_INVALID_ARGUMENT, "tile of %u keys too large for look-back groups", tile);
-    a.tiles_per_portion = tpp;
+    a.wide = wide ? 1u : 0u;
     a.tile = tile;
     a.vec_ok = ((uintptr_t)keys % 16 == 0) ? 1u : 0u;
     // upsweep: about 4 blocks per CU over contiguous runs of tiles
@@ -419,7 +420,7 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
             if (s->tile[i] == 0 || s->block[i] < FS_RADIX)
                 return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object has an invalid tile geometry");
     }
-    const size_t tab = (size_t)FS_MAX_PORTIONS * FS_MAX_DIGITS * FS_RADIX * 4;
+    const size_t tab = (size_t)FS_MAX_DIGITS * FS_RADIX * 4;
     if (hipMalloc(&s->hist, tab) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||
         hipMalloc(&s->tile_ctr, FS_MAX_DIGITS * 4) != hipSuccess ||
         hipMalloc(&s->plan, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||

@@ -46,31 +46,25 @@
 // Upsweep (all-digit histogram) block.
 #define FS_HIST_BLOCK 256
 
-// Look-back entries: one 32-bit word per (tile, digit) = [flag:2 | count:30].
-// Counts are kept below 2^30 by splitting the input into portions of at most
-// 2^30 keys; each portion has its own look-back chain and bin bases.
+// Look-back tile entries, one per (tile, digit), in a single chain over all
+// tiles: a 32-bit word [flag:2 | value:30] when n < FS_LB_WIDE_KEYS, else a
+// 64-bit word whose high half holds the flag bits and low half the value (an
+// inclusive prefix can then exceed 30 bits).  Counts of one tile or group are
+// far below 2^30 either way.
 #define FS_LB_AGG 0x40000000u
 #define FS_LB_INC 0x80000000u
 #define FS_LB_FLAGS 0xC0000000u
 #define FS_LB_VALUE 0x3FFFFFFFu
-#define FS_PORTION_KEYS (1u << 30)
-// A portion is the largest power-of-two number of tiles holding at most 2^30
-// keys, so it holds more than 2^29 keys and n < 2^32 needs fewer than 8.
-#define FS_MAX_PORTIONS 8
-
-// Order of a tile's look-back: 2 = histogram, publish the aggregate, look back
-// and publish the inclusive prefix, then rank; 0 = rank first and publish the
-// ranking's wave counts afterwards.
-#ifndef FS_EARLY_AGG
-#define FS_EARLY_AGG 2
+#ifndef FS_LB_WIDE_KEYS
+#define FS_LB_WIDE_KEYS (1u << 30)
 #endif
 
 // Predecessor tile entries read per look-back round trip.
 #ifndef FS_LB_WINDOW
 #define FS_LB_WINDOW 4
 #endif
-// Second look-back level: FS_LB_GROUP consecutive tiles (a power of two that
-// divides tiles_per_portion) share a group entry per digit holding
+// Second look-back level: FS_LB_GROUP consecutive tiles (a power of two)
+// share a group entry per digit holding
 // (tiles added << FS_LB_GCOUNT_SHIFT) | sum of their counts; FS_LB_GWIN groups
 // are read per round trip.  FS_LB_GROUP * tile keys < 2^24 keeps the sum in
 // its field.
@@ -142,7 +136,7 @@ typedef struct FsArgs {
     uint32_t op;                // FSK_OP_*
     uint32_t digits;            // 4 or 8
     uint32_t num_tiles;         // ceil(n / tile)
-    uint32_t tiles_per_portion; // power of two, tiles_per_portion * tile <= FS_PORTION_KEYS
+    uint32_t wide;              // 1: 64-bit look-back tile entries (n >= FS_LB_WIDE_KEYS)
     uint32_t hist_tiles_per_block;  // tiles per upsweep block
     uint32_t tile;              // keys per tile of the digit-pass variant in use
     uint32_t vec_ok;            // keys pointer is 16-byte aligned
@@ -150,9 +144,10 @@ typedef struct FsArgs {
     uint64_t keys;              // caller keys (in place for KEYS/PAIRS; read-only for ARGSORT)
     uint64_t vals;              // caller values (PAIRS) or output indices (ARGSORT)
     uint64_t s1k, s2k, s1v, s2v;   // scratch ping-pong buffers
-    uint64_t hist;              // u32 [FS_MAX_PORTIONS][digits][256], zero between sorts
-    uint64_t binbase;           // u32 [FS_MAX_PORTIONS][digits][256]
-    uint64_t lookback0, lookback1;  // u32 [num_tiles][256] each
+    uint64_t hist;              // u32 [digits][256], zero between sorts
+    uint64_t binbase;           // u32 [digits][256]
+    uint64_t lookback0, lookback1;  // [num_tiles][256] tile entries (u32, or u64 when wide),
+                                    // then u32 [groups][256] group entries; alternate per pass
     uint64_t tile_ctr;          // u32 [FS_MAX_DIGITS]
     uint64_t plan;              // u32[FS_PLAN_WORDS] schedule
     uint64_t status;            // u32, host-visible error bits

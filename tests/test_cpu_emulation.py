@@ -80,3 +80,13 @@ def test_emulated_lookback_groups(emulator):
     run_cases("groups", ["sort:u32:70000:uniform:2", "sort:i64:9000:uniform:3", "argsort:f32:33333:few:4",
                          "pairs:u64:5000:low12:5", "sort:u32:1025:uniform:6", "pairs:u32:40000:uniform:7"],
               env={"EMU_CUS": "8"})
+
+
+
+@pytest.mark.parametrize("flavor", ["small", "groups"])
+def test_emulated_wide_lookback_entries(emulator, flavor):
+    """The 64-bit look-back tile entries used from n = 2^30 on, forced for
+    small inputs (FS_LB_FORCE_WIDE=1)."""
+    run_cases(flavor, ["sort:u32:70000:uniform:2", "sort:i64:9000:uniform:3", "argsort:f32:33333:few:4",
+                       "pairs:u64:5000:low12:5", "pairs:u32:40000:uniform:7"],
+              env={"EMU_CUS": "8", "FS_LB_FORCE_WIDE": "1"})

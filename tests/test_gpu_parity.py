@@ -288,3 +288,40 @@ def test_config4_64bit(sorter, kind):
         check_buffer(sorter, "u64", datagen.low20_u64(n, high=0, seed=110))
     else:
         check_buffer(sorter, "u64", datagen.low20_u64(n, high=0xABCDEF01234, seed=111))
+
+
+@pytest.fixture
+def force_wide_lookback():
+    """Select the 64-bit look-back tile entries (normally used from n = 2^30
+    on) for every sort of the test; the library reads the switch per call."""
+    os.environ["FS_LB_FORCE_WIDE"] = "1"
+    yield
+    del os.environ["FS_LB_FORCE_WIDE"]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_wide_lookback_entries(sorter, force_wide_lookback, kind):
+    n = 1_000_003
+    check_sort(sorter, kind, make_keys(kind, n, "uniform", seed=400))
+    check_argsort(sorter, kind, make_keys(kind, 70_001, "few", seed=401))
+    check_pairs(sorter, kind, make_keys(kind, 100_000, "uniform", seed=402),
+                np.arange(100_000, dtype=np.uint32)[::-1].copy())
+
+
+def test_more_than_2_30_keys(sorter):
+    """n = 2^30 + 12345 u32 keys: inclusive prefixes exceed 30 bits, so the
+    64-bit look-back entries are in use.  Checked without the oracle (too slow
+    at this size) by properties that fix the result: ascending order and equal
+    multisets (sum, xor and sum of squares mod 2^64 of the keys)."""
+    n = (1 << 30) + 12345
+    keys = datagen.uniform_u32(n, seed=500)
+    buf = sorter.alloc_sort_buffer("u32", n)
+    buf.copy_from_slice(keys)
+    sorter.sort_buffer(buf)
+    out = buf.as_slice()
+    buf.free()
+    assert bool(np.all(out[1:] >= out[:-1])), "not ascending"
+    k64, o64 = keys.astype(np.uint64), out.astype(np.uint64)
+    assert int(k64.sum()) == int(o64.sum())
+    assert int(np.bitwise_xor.reduce(keys)) == int(np.bitwise_xor.reduce(out))
+    assert int((k64 * k64).sum()) == int((o64 * o64).sum())
