@@ -46,9 +46,27 @@ def keys_for(kind, n, dist, seed):
     return b.view(oracle.NP_DTYPES[kind])
 
 
+def check_offset(sorter, kind, keys):
+    """Sort keys that start one element past a 16-byte boundary (device API):
+    the upsweep then reads them one key at a time."""
+    import ctypes
+    n, size = keys.size, keys.itemsize
+    buf = sorter.alloc_sort_buffer(kind, n + 1)
+    ptr = buf.device_ptr() + size
+    L = forge_sort._load()
+    sorter._check(L.fs_copy_to_device(sorter._h, ctypes.c_void_p(ptr), keys.ctypes.data, n * size))
+    sorter.sort_device(kind, ptr, n)
+    out = np.empty_like(keys)
+    sorter._check(L.fs_copy_to_host(sorter._h, out.ctypes.data, ctypes.c_void_p(ptr), n * size))
+    buf.free()
+    return np.array_equal(out.view(BITS[kind]), oracle.sort(kind, keys).view(BITS[kind]))
+
+
 def check(sorter, op, kind, n, dist, seed):
     keys = keys_for(kind, n, dist, seed)
-    if op == "sort":
+    if op == "offset":
+        ok = check_offset(sorter, kind, keys)
+    elif op == "sort":
         got = keys.copy()
         getattr(sorter, f"sort_{kind}")(got)
         ok = np.array_equal(got.view(BITS[kind]), oracle.sort(kind, keys).view(BITS[kind]))
@@ -61,6 +79,8 @@ def check(sorter, op, kind, n, dist, seed):
         getattr(sorter, f"sort_pairs_{kind}")(gk, gv)
         ok = np.array_equal(gk.view(BITS[kind]), ek.view(BITS[kind])) and np.array_equal(gv, ev)
     passes, mask = sorter.last_pass_info()
+    if dist == "same" and op != "offset" and n > 1:
+        ok = ok and passes == 0 and mask == 0     # every digit constant: an exact histogram says so
     print(f"{'PASS' if ok else 'FAIL'} {op} {kind} n={n} {dist} passes={passes} mask={mask:#x}", flush=True)
     return ok
 

@@ -90,3 +90,15 @@ def test_emulated_wide_lookback_entries(emulator, flavor):
     run_cases(flavor, ["sort:u32:70000:uniform:2", "sort:i64:9000:uniform:3", "argsort:f32:33333:few:4",
                        "pairs:u64:5000:low12:5", "pairs:u32:40000:uniform:7"],
               env={"EMU_CUS": "8", "FS_LB_FORCE_WIDE": "1"})
+
+
+def test_emulated_upsweep_long_segments(emulator):
+    """One upsweep block per emulated CU, one CU: each block counts a long
+    segment; all-equal keys must come out with every digit constant (an exact
+    histogram, so no pass runs); keys one element past a 16-byte boundary take
+    the upsweep's one-key-at-a-time path."""
+    cases = ["sort:u32:200000:uniform:1", "sort:u32:150000:same:2", "sort:u64:90000:same:3",
+             "sort:i64:70001:uniform:4", "offset:u32:100003:uniform:5", "offset:u64:50001:few:6",
+             "offset:f32:3:uniform:7"]
+    for flavor in ("small", "prod"):
+        run_cases(flavor, cases, env={"EMU_CUS": "1", "FS_UPSWEEP_BLOCKS_PER_CU": "1"})
