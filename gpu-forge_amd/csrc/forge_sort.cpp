@@ -677,4 +677,163 @@ fs_status fs_profile_read(fs_sorter* s, int index, const char** kernel_name, flo
     return FS_OK;
 }
 
+// ---------------------------------------------------------------------------
+// GpuGather (forge-runtime/src/gather.rs:26-173): output[i] = source[indices[i]]
+// for u32 or u64 elements, with its own stream (or the caller's) and the same
+// code object as the sorter.
+// ---------------------------------------------------------------------------
+
+struct fs_gather {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    hipModule_t module = nullptr;
+    hipFunction_t fn = nullptr;
+    uint32_t* status = nullptr;     // host-visible error bits (hipHostMalloc)
+    int num_cus = 256;
+    hipStream_t last_stream = nullptr;
+    bool pending = false;
+    std::string err;
+};
+
+static fs_status gather_err(fs_gather* g, fs_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (g) g->err = display(st, buf);
+    return st;
+}
+
+#define GATHER_TRY(g, call)                                                                \
+    do {                                                                                   \
+        hipError_t e_ = (call);                                                            \
+        if (e_ != hipSuccess)                                                              \
+            return gather_err((g), FS_ERR_GPU_EXECUTION, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+static fs_status gather_create(int device, hipStream_t stream, bool own, fs_gather** out) {
+    if (!out) return create_failed(nullptr, FS_ERR_INVALID_ARGUMENT, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0 || device < 0 || device >= count) {
+        (void)hipGetLastError();
+        return create_failed(nullptr, FS_ERR_DEVICE_NOT_FOUND, "");
+    }
+    fs_gather* g = new (std::nothrow) fs_gather();
+    if (!g) return create_failed(nullptr, FS_ERR_OUT_OF_MEMORY, "host allocation of the gather");
+    g->device = device;
+    hipError_t e = hipSetDevice(device);
+    int cus = 0;
+    if (e == hipSuccess && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+        cus > 0)
+        g->num_cus = cus;
+    if (e == hipSuccess && own) {
+        e = hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking);
+        g->own_stream = e == hipSuccess;
+    } else if (e == hipSuccess) {
+        g->stream = stream;
+    }
+    g->last_stream = g->stream;
+    const std::string path = code_object_path();
+    if (e == hipSuccess) e = hipModuleLoad(&g->module, path.c_str());
+    if (e == hipSuccess) e = hipModuleGetFunction(&g->fn, g->module, "fs_gather_elems");
+    if (e == hipSuccess) e = hipHostMalloc((void**)&g->status, sizeof(uint32_t), hipHostMallocDefault);
+    if (e != hipSuccess) {
+        const std::string msg = "loading " + path + ": " + hipGetErrorString(e);
+        fs_gather_free(g);
+        return create_failed(nullptr, FS_ERR_SHADER_COMPILATION, msg);
+    }
+    *g->status = 0;
+    *out = g;
+    return FS_OK;
+}
+
+fs_status fs_gather_new(int device, fs_gather** out) { return gather_create(device, nullptr, true, out); }
+
+fs_status fs_gather_with_context(int device, void* hip_stream, fs_gather** out) {
+    return gather_create(device, (hipStream_t)hip_stream, false, out);
+}
+
+void fs_gather_free(fs_gather* g) {
+    if (!g) return;
+    (void)hipSetDevice(g->device);
+    if (g->pending) (void)hipStreamSynchronize(g->last_stream);
+    if (g->status) (void)hipHostFree(g->status);
+    if (g->module) (void)hipModuleUnload(g->module);
+    if (g->own_stream && g->stream) (void)hipStreamDestroy(g->stream);
+    delete g;
+}
+
+const char* fs_gather_last_error(const fs_gather* g) { return g ? g->err.c_str() : g_create_err.c_str(); }
+
+fs_status fs_gather_alloc_buffer(fs_gather* g, size_t bytes, void** device_ptr) {
+    if (!g || !device_ptr) return FS_ERR_INVALID_ARGUMENT;
+    *device_ptr = nullptr;
+    GATHER_TRY(g, hipSetDevice(g->device));
+    if (hipMalloc(device_ptr, bytes ? bytes : 1) != hipSuccess) {
+        (void)hipGetLastError();
+        *device_ptr = nullptr;
+        return gather_err(g, FS_ERR_OUT_OF_MEMORY, "hipMalloc(%zu) failed", bytes);
+    }
+    return FS_OK;
+}
+
+fs_status fs_gather_free_buffer(fs_gather* g, void* device_ptr) {
+    if (!g) return FS_ERR_INVALID_ARGUMENT;
+    if (device_ptr) GATHER_TRY(g, hipFree(device_ptr));
+    return FS_OK;
+}
+
+fs_status fs_gather_encode(fs_gather* g, int is_64bit, const void* source, uint64_t source_len,
+                           const uint32_t* indices, void* output, uint64_t count, void* hip_stream) {
+    if (!g) return FS_ERR_INVALID_ARGUMENT;
+    if (count == 0) return FS_OK;
+    if (!source || !indices || !output)
+        return gather_err(g, FS_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (count >= (1ull << 32) || source_len > (1ull << 32))
+        return gather_err(g, FS_ERR_INVALID_ARGUMENT, "count or source length beyond u32 indices");
+    GATHER_TRY(g, hipSetDevice(g->device));
+    hipStream_t st = hip_stream ? (hipStream_t)hip_stream : g->stream;
+    if (g->pending && g->last_stream != st) GATHER_TRY(g, hipStreamSynchronize(g->last_stream));
+    uint64_t blocks = (count + 255) / 256;
+    if (blocks > (uint64_t)g->num_cus * 16) blocks = (uint64_t)g->num_cus * 16;
+    uint64_t src = (uint64_t)(uintptr_t)source, idx = (uint64_t)(uintptr_t)indices;
+    uint64_t dst = (uint64_t)(uintptr_t)output, stat = (uint64_t)(uintptr_t)g->status;
+    uint32_t is64 = is_64bit ? 1u : 0u;
+    void* args[] = {&src, &source_len, &idx, &dst, &count, &is64, &stat};
+    GATHER_TRY(g, hipModuleLaunchKernel(g->fn, (unsigned)blocks, 1, 1, 256, 1, 1, 0, st, args, nullptr));
+    g->last_stream = st;
+    g->pending = true;
+    return FS_OK;
+}
+
+fs_status fs_gather_synchronize(fs_gather* g) {
+    if (!g) return FS_ERR_INVALID_ARGUMENT;
+    GATHER_TRY(g, hipSetDevice(g->device));
+    if (g->pending) GATHER_TRY(g, hipStreamSynchronize(g->last_stream));
+    g->pending = false;
+    const uint32_t st = __atomic_load_n(g->status, __ATOMIC_ACQUIRE);
+    if (st) {
+        __atomic_store_n(g->status, 0u, __ATOMIC_RELEASE);
+        if (st & FS_DEVERR_GATHER_INDEX)
+            return gather_err(g, FS_ERR_GPU_EXECUTION, "gather index out of range of the source");
+        return gather_err(g, FS_ERR_GPU_EXECUTION, "device status 0x%x", st);
+    }
+    return FS_OK;
+}
+
+fs_status fs_gather_u32(fs_gather* g, const uint32_t* source, uint64_t source_len, const uint32_t* indices,
+                        uint32_t* output, uint64_t count) {
+    fs_status r = fs_gather_encode(g, 0, source, source_len, indices, output, count, nullptr);
+    return r != FS_OK ? r : fs_gather_synchronize(g);
+}
+
+fs_status fs_gather_u64(fs_gather* g, const uint64_t* source, uint64_t source_len, const uint32_t* indices,
+                        uint64_t* output, uint64_t count) {
+    fs_status r = fs_gather_encode(g, 1, source, source_len, indices, output, count, nullptr);
+    return r != FS_OK ? r : fs_gather_synchronize(g);
+}
+
 }  // extern "C"

@@ -127,6 +127,7 @@
 // Error bits additionally reported through the status word.
 #define FS_DEVERR_BAD_TILE 2u        // a digit pass drew a tile id >= num_tiles
 #define FS_DEVERR_BAD_PLAN 4u        // a schedule named a buffer the call does not have
+#define FS_DEVERR_GATHER_INDEX 8u    // a gather index was >= the source length
 
 // Kernel argument block, passed by value to every kernel.
 typedef struct FsArgs {

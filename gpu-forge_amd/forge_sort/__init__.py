@@ -23,6 +23,7 @@ import numpy as np
 from . import _build
 
 __all__ = [
+    "GpuGather",
     "GpuSorter", "SortBuffer", "SortError", "DeviceNotFound", "ShaderCompilation",
     "GpuExecution", "LengthMismatch", "KEY_TYPES", "library_path",
 ]
@@ -130,6 +131,16 @@ def _load():
         "fs_tile_config": ([vp, u32p], i),
         "fs_set_lookback_stats": ([vp, i], i),
         "fs_read_lookback_stats": ([vp, ctypes.POINTER(ctypes.c_uint64)], i),
+        "fs_gather_new": ([i, pp], i),
+        "fs_gather_with_context": ([i, vp, pp], i),
+        "fs_gather_free": ([vp], None),
+        "fs_gather_last_error": ([vp], ctypes.c_char_p),
+        "fs_gather_alloc_buffer": ([vp, sz, pp], i),
+        "fs_gather_free_buffer": ([vp, vp], i),
+        "fs_gather_encode": ([vp, i, vp, u64, vp, vp, u64, vp], i),
+        "fs_gather_synchronize": ([vp], i),
+        "fs_gather_u32": ([vp, vp, u64, vp, vp, u64], i),
+        "fs_gather_u64": ([vp, vp, u64, vp, vp, u64], i),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -443,3 +454,73 @@ class GpuSorter:
         return out
 
 
+
+
+class GpuGather:
+    """GpuGather (forge-runtime/src/gather.rs:26-173): output[i] = source[indices[i]]
+    for u32 or u64 elements on device memory.  Pointers are device addresses
+    (GpuGather.alloc_buffer, SortBuffer.device_ptr(), a torch tensor's data_ptr()).
+    source_len bounds the indices: an index past it yields 0 and raises
+    GpuExecution (the reference reads out of bounds)."""
+
+    def __init__(self, device=0, stream=None, _with_context=False):
+        L = _load()
+        h = ctypes.c_void_p()
+        if _with_context:
+            st = L.fs_gather_with_context(device, ctypes.c_void_p(stream), ctypes.byref(h))
+        else:
+            st = L.fs_gather_new(device, ctypes.byref(h))
+        if st != FS_OK:
+            msg = L.fs_gather_last_error(None).decode() or L.fs_status_str(st).decode()
+            raise _ERRORS.get(st, SortError)(msg)
+        self._h = h
+        self.device = device
+
+    @classmethod
+    def new(cls, device=0):
+        return cls(device)
+
+    @classmethod
+    def with_context(cls, device, stream):
+        return cls(device, stream, _with_context=True)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _load().fs_gather_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st):
+        if st != FS_OK:
+            raise _ERRORS.get(st, SortError)(_load().fs_gather_last_error(self._h).decode())
+
+    def alloc_buffer(self, nbytes):
+        """GpuGather::alloc_buffer: device memory; returns its address."""
+        p = ctypes.c_void_p()
+        self._check(_load().fs_gather_alloc_buffer(self._h, nbytes, ctypes.byref(p)))
+        return p.value
+
+    def free_buffer(self, ptr):
+        self._check(_load().fs_gather_free_buffer(self._h, ctypes.c_void_p(ptr)))
+
+    def encode_gather(self, source_ptr, indices_ptr, output_ptr, count, is_64bit, source_len, stream=None):
+        """encode_gather (gather.rs:81-119): enqueue, no wait."""
+        self._check(_load().fs_gather_encode(self._h, 1 if is_64bit else 0, ctypes.c_void_p(source_ptr),
+                                             source_len, ctypes.c_void_p(indices_ptr),
+                                             ctypes.c_void_p(output_ptr), count, ctypes.c_void_p(stream or 0)))
+
+    def synchronize(self):
+        self._check(_load().fs_gather_synchronize(self._h))
+
+    def gather_u32(self, source_ptr, indices_ptr, output_ptr, count, source_len):
+        self._check(_load().fs_gather_u32(self._h, ctypes.c_void_p(source_ptr), source_len,
+                                          ctypes.c_void_p(indices_ptr), ctypes.c_void_p(output_ptr), count))
+
+    def gather_u64(self, source_ptr, indices_ptr, output_ptr, count, source_len):
+        self._check(_load().fs_gather_u64(self._h, ctypes.c_void_p(source_ptr), source_len,
+                                          ctypes.c_void_p(indices_ptr), ctypes.c_void_p(output_ptr), count))

@@ -171,6 +171,44 @@ fs_status fs_read_lookback_stats(fs_sorter *s, uint64_t counters[4]);
  * object: [u32 keys, u32 keys + values, u64 keys, u64 keys + values]. */
 fs_status fs_tile_config(const fs_sorter *s, uint32_t keys_per_tile[4]);
 
+/* ---- GpuGather (forge-runtime/src/gather.rs:26-173) --------------------------
+ * output[i] = source[indices[i]] for u32 or u64 elements, u32 indices
+ * (shaders/gather.metal:5-27).  The reference reads past the source for an
+ * index out of range; here the source length is passed, such an element comes
+ * out 0, and the next fs_gather_synchronize reports FS_ERR_GPU_EXECUTION. */
+typedef struct fs_gather fs_gather;
+
+/* GpuGather::new (gather.rs:38-46): device `device`, a stream of its own. */
+fs_status fs_gather_new(int device, fs_gather **out);
+
+/* GpuGather::with_context (gather.rs:49-72): the caller's HIP stream (not owned). */
+fs_status fs_gather_with_context(int device, void *hip_stream, fs_gather **out);
+
+/* Drop for GpuGather. */
+void fs_gather_free(fs_gather *g);
+
+/* Message of the last failing call (NULL: the last failed fs_gather_new /
+ * fs_gather_with_context on this thread). */
+const char *fs_gather_last_error(const fs_gather *g);
+
+/* GpuGather::alloc_buffer (gather.rs:169-173): device memory of `bytes`. */
+fs_status fs_gather_alloc_buffer(fs_gather *g, size_t bytes, void **device_ptr);
+fs_status fs_gather_free_buffer(fs_gather *g, void *device_ptr);
+
+/* encode_gather (gather.rs:81-119): enqueue on hip_stream (NULL = the gather's
+ * own) and return without waiting; `is_64bit` selects u64 elements. */
+fs_status fs_gather_encode(fs_gather *g, int is_64bit, const void *source, uint64_t source_len,
+                           const uint32_t *indices, void *output, uint64_t count, void *hip_stream);
+
+/* Wait for the last encode; report an out-of-range index. */
+fs_status fs_gather_synchronize(fs_gather *g);
+
+/* gather_u32 (gather.rs:124-132) and gather_u64 (:135-143): encode and wait. */
+fs_status fs_gather_u32(fs_gather *g, const uint32_t *source, uint64_t source_len, const uint32_t *indices,
+                        uint32_t *output, uint64_t count);
+fs_status fs_gather_u64(fs_gather *g, const uint64_t *source, uint64_t source_len, const uint32_t *indices,
+                        uint64_t *output, uint64_t count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -282,3 +282,26 @@ int or_sort_pairs(int kt, void *keys, uint64_t n_keys, uint32_t *vals, uint64_t 
         apply(kt, keys, n, inv_mode(kt));
     return OR_OK;
 }
+
+/* GpuGather: output[i] = source[indices[i]] for u32 / u64 elements
+ * (metal-forge-compute/forge-runtime/shaders/gather.metal:5-27, driven by
+ * src/gather.rs:81-143).  The reference has no bounds check; here an index at
+ * or past source_len yields OR_ERR_INVALID_ARGUMENT (the product reports it as
+ * a GPU execution error and writes 0 there).  Mutation 6 reads the next
+ * element instead. */
+int or_gather(int is64, const void *source, uint64_t source_len, const uint32_t *indices, void *output,
+              uint64_t count) {
+    int bad = 0;
+    for (uint64_t i = 0; i < count; ++i) {
+        uint64_t j = indices[i];
+        if (or_mutation == 6 && j + 1 < source_len) ++j;
+        if (j >= source_len) {
+            bad = 1;
+            if (is64) ((uint64_t *)output)[i] = 0; else ((uint32_t *)output)[i] = 0;
+            continue;
+        }
+        if (is64) ((uint64_t *)output)[i] = ((const uint64_t *)source)[j];
+        else ((uint32_t *)output)[i] = ((const uint32_t *)source)[j];
+    }
+    return bad ? OR_ERR_INVALID_ARGUMENT : OR_OK;
+}

@@ -4,7 +4,8 @@ TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 cpu_baseline leg of bench.py, never by the product package.  The functions
 mirror GpuSorter's host entry points (metal-forge-compute/forge-sort/src/lib.rs:
 sort_<t> :791/:840/:920/:2238/:2348/:2417, argsort_<t> :1675/:1754/:1838/:2595/
-:2669/:2747, sort_pairs_<t> :1923/:2024/:2132/:2826/:2921) on numpy arrays.
+:2669/:2747, sort_pairs_<t> :1923/:2024/:2132/:2826/:2921) on numpy arrays, and
+forge-runtime's GpuGather (src/gather.rs:124-143).
 """
 import ctypes
 import os
@@ -42,7 +43,8 @@ def lib():
         L.or_sort_pairs.argtypes = [ctypes.c_int, vp, u64, vp, u64]
         L.or_transform_32.argtypes = [vp, u64, ctypes.c_uint32]
         L.or_transform_64.argtypes = [vp, u64, ctypes.c_uint32]
-        for f in (L.or_sort, L.or_argsort, L.or_sort_pairs):
+        L.or_gather.argtypes = [ctypes.c_int, vp, u64, vp, vp, u64]
+        for f in (L.or_sort, L.or_argsort, L.or_sort_pairs, L.or_gather):
             f.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -103,3 +105,19 @@ def transform(bits, mode):
     else:
         raise TypeError("transform takes uint32 or uint64 bit patterns")
     return b
+
+
+def gather(source, indices):
+    """GpuGather::gather_u32 / gather_u64: source[indices] for a u32 or u64
+    source array; raises IndexError for an index past the source (the product
+    reports GpuExecution and writes 0 there)."""
+    source = np.ascontiguousarray(source)
+    if source.dtype not in (np.uint32, np.uint64):
+        raise TypeError("gather source must be u32 or u64")
+    indices = np.ascontiguousarray(indices, dtype=np.uint32)
+    out = np.zeros(indices.size, dtype=source.dtype)
+    st = lib().or_gather(1 if source.dtype == np.uint64 else 0, _ptr(source), source.size,
+                         _ptr(indices), _ptr(out), indices.size)
+    if st != OK:
+        raise IndexError("gather index out of range of the source")
+    return out

@@ -62,7 +62,33 @@ def check_offset(sorter, kind, keys):
     return np.array_equal(out.view(BITS[kind]), oracle.sort(kind, keys).view(BITS[kind]))
 
 
+def check_gather(kind, n, seed):
+    """GpuGather on random indices (u32 or u64 elements by key width)."""
+    import ctypes
+    g = np.random.Generator(np.random.PCG64(seed))
+    src = g.integers(0, 1 << 63, size=n, dtype=np.uint64).astype(BITS[kind])
+    idx = g.integers(0, n, size=n + 5, dtype=np.uint32)
+    ga = forge_sort.GpuGather.new()
+    ps, pi, po = ga.alloc_buffer(src.nbytes), ga.alloc_buffer(idx.nbytes), ga.alloc_buffer(idx.size * src.itemsize)
+    L = forge_sort._load()
+    s = forge_sort.GpuSorter.new()
+    s._check(L.fs_copy_to_device(s._h, ctypes.c_void_p(ps), src.ctypes.data, src.nbytes))
+    s._check(L.fs_copy_to_device(s._h, ctypes.c_void_p(pi), idx.ctypes.data, idx.nbytes))
+    (ga.gather_u64 if src.dtype == np.uint64 else ga.gather_u32)(ps, pi, po, idx.size, src.size)
+    out = np.empty(idx.size, dtype=src.dtype)
+    s._check(L.fs_copy_to_host(s._h, out.ctypes.data, ctypes.c_void_p(po), out.nbytes))
+    for p in (ps, pi, po):
+        ga.free_buffer(p)
+    ga.close()
+    s.close()
+    return np.array_equal(out, oracle.gather(src, idx))
+
+
 def check(sorter, op, kind, n, dist, seed):
+    if op == "gather":
+        ok = check_gather(kind, n, seed)
+        print(f"{'PASS' if ok else 'FAIL'} gather {kind} n={n}", flush=True)
+        return ok
     keys = keys_for(kind, n, dist, seed)
     if op == "offset":
         ok = check_offset(sorter, kind, keys)

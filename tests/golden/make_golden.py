@@ -248,6 +248,27 @@ add_pairs("pairs_spec_negzero_stability", FS + "ai/tasks/spec/QA.md:542", "f32",
           [0x80000000, 0, 0x80000000, 0], [0, 1, 2, 3],
           [0x80000000, 0x80000000, 0, 0], [0, 2, 1, 3])
 
+# GpuGather known answers (forge-runtime/src/gather.rs tests): output[i] = source[indices[i]]
+RT = "metal-forge-compute/forge-runtime/"
+
+
+def add_gather(name, src, kind, source, indices, expected):
+    computed = [source[i] for i in indices]
+    assert computed == expected, name
+    cases.append({"name": name, "source": src, "op": "gather", "type": kind,
+                  "values": source, "indices": indices, "expected_values": computed,
+                  "expected_from": "reference"})
+
+
+add_gather("gather_u32_permutation", RT + "src/gather.rs:213-248", "u32",
+           [10, 20, 30, 40], [2, 0, 1, 3], [30, 10, 20, 40])
+add_gather("gather_u64_permutation", RT + "src/gather.rs:251-286", "u64",
+           [100, 200, 300, 400], [3, 1, 0, 2], [400, 200, 100, 300])
+add_gather("gather_u32_identity", RT + "src/gather.rs:289-324", "u32",
+           [(i + 1) * 10 for i in range(5)], list(range(5)), [(i + 1) * 10 for i in range(5)])
+add_gather("gather_u32_reverse", RT + "src/gather.rs:327-363", "u32",
+           [i * 100 for i in range(8)], list(range(7, -1, -1)), [i * 100 for i in range(7, -1, -1)])
+
 if __name__ == "__main__":
     out = os.path.join(HERE, "golden.json")
     with open(out, "w") as f:

@@ -55,6 +55,8 @@ SMALL_CASES = [
     "sort:u32:0:uniform:19", "sort:u32:1:uniform:20", "sort:u32:2:uniform:21",
     "sort:u32:63:uniform:22", "sort:u32:65:uniform:23", "pairs:u64:3:uniform:24",
     "argsort:f64:1025:uniform:25",
+    # GpuGather
+    "gather:u32:5000:uniform:26", "gather:u64:3001:uniform:27",
 ]
 
 PROD_CASES = [

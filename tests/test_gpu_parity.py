@@ -84,7 +84,11 @@ def load_golden():
         return json.load(f)["cases"]
 
 
-@pytest.mark.parametrize("case", load_golden(), ids=lambda c: c["name"])
+def golden_sort_cases():
+    return [c for c in load_golden() if c["op"] != "gather"]
+
+
+@pytest.mark.parametrize("case", golden_sort_cases(), ids=lambda c: c["name"])
 def test_golden(sorter, case):
     kind = case["type"]
     keys = np.array(case["keys"], dtype=BITS[kind]).view(NP[kind])
@@ -325,3 +329,97 @@ def test_more_than_2_30_keys(sorter):
     assert int(k64.sum()) == int(o64.sum())
     assert int(np.bitwise_xor.reduce(keys)) == int(np.bitwise_xor.reduce(out))
     assert int((k64 * k64).sum()) == int((o64 * o64).sum())
+
+
+@pytest.mark.parametrize("kind", ["u32", "f32", "u64", "i64"])
+def test_device_keys_off_16_byte_boundary(sorter, kind):
+    """Keys one element past a 16-byte boundary (e.g. a slice of a larger
+    device array): the upsweep reads them one at a time."""
+    import ctypes
+    import forge_sort
+    n = 300_007
+    keys = make_keys(kind, n, "uniform", seed=600)
+    size = keys.itemsize
+    buf = sorter.alloc_sort_buffer(kind, n + 1)
+    ptr = buf.device_ptr() + size
+    L = forge_sort._load()
+    sorter._check(L.fs_copy_to_device(sorter._h, ctypes.c_void_p(ptr), keys.ctypes.data, n * size))
+    sorter.sort_device(kind, ptr, n)
+    out = np.empty_like(keys)
+    sorter._check(L.fs_copy_to_host(sorter._h, out.ctypes.data, ctypes.c_void_p(ptr), n * size))
+    buf.free()
+    exp = oracle.sort(kind, keys)
+    assert bits_equal(out, exp, kind), first_diff(out, exp, kind)
+
+
+
+# ---- GpuGather (forge-runtime/src/gather.rs) ----------------------------------
+
+@pytest.fixture(scope="module")
+def gatherer():
+    from forge_sort import GpuGather
+    g = GpuGather.new()
+    yield g
+    g.close()
+
+
+def gpu_gather(gatherer, src, idx):
+    """Device copies of src and idx, gather, copy back (through the library)."""
+    import ctypes
+    import forge_sort
+    L = forge_sort._load()
+    is64 = src.dtype == np.uint64
+    ps = gatherer.alloc_buffer(max(1, src.nbytes))
+    pi = gatherer.alloc_buffer(max(1, idx.nbytes))
+    po = gatherer.alloc_buffer(max(1, idx.size * src.itemsize))
+    try:
+        with_sorter = forge_sort.GpuSorter.new()
+        with_sorter._check(L.fs_copy_to_device(with_sorter._h, ctypes.c_void_p(ps), src.ctypes.data, src.nbytes))
+        with_sorter._check(L.fs_copy_to_device(with_sorter._h, ctypes.c_void_p(pi), idx.ctypes.data, idx.nbytes))
+        (gatherer.gather_u64 if is64 else gatherer.gather_u32)(ps, pi, po, idx.size, src.size)
+        out = np.empty(idx.size, dtype=src.dtype)
+        with_sorter._check(L.fs_copy_to_host(with_sorter._h, out.ctypes.data, ctypes.c_void_p(po),
+                                             idx.size * src.itemsize))
+        with_sorter.close()
+        return out
+    finally:
+        for p in (ps, pi, po):
+            gatherer.free_buffer(p)
+
+
+@pytest.mark.parametrize("case", [c for c in load_golden() if c["op"] == "gather"], ids=lambda c: c["name"])
+def test_gather_golden(gatherer, case):
+    src = np.array(case["values"], dtype=BITS[case["type"]])
+    got = gpu_gather(gatherer, src, np.array(case["indices"], dtype=np.uint32))
+    assert got.tolist() == case["expected_values"]
+
+
+@pytest.mark.parametrize("dtype", [np.uint32, np.uint64])
+@pytest.mark.parametrize("n", [1, 255, 100_003, 4_000_000])
+def test_gather_random(gatherer, dtype, n):
+    g = np.random.Generator(np.random.PCG64(n))
+    src = g.integers(0, 1 << 63, size=n, dtype=np.uint64).astype(dtype)
+    idx = g.integers(0, n, size=n + 17, dtype=np.uint32)
+    assert np.array_equal(gpu_gather(gatherer, src, idx), oracle.gather(src, idx))
+
+
+def test_gather_index_out_of_range(gatherer):
+    from forge_sort import GpuExecution
+    src = np.arange(10, dtype=np.uint32)
+    with pytest.raises(GpuExecution, match="out of range"):
+        gpu_gather(gatherer, src, np.array([0, 10, 3], dtype=np.uint32))
+    # the gather stays usable afterwards
+    assert gpu_gather(gatherer, src, np.array([9, 0], dtype=np.uint32)).tolist() == [9, 0]
+
+
+def test_sort_then_gather(sorter, gatherer):
+    """forge-runtime's sort -> gather pipeline (tests/pipeline_tests.rs:168-205):
+    argsort a column, gather a second column through the permutation; the
+    result equals the pairs sort of the same data."""
+    n = 100_000
+    g = np.random.Generator(np.random.PCG64(77))
+    keys = g.integers(0, 1000, size=n, dtype=np.uint32)
+    other = g.integers(0, 1 << 63, size=n, dtype=np.uint64)
+    perm = sorter.argsort_u32(keys)
+    got = gpu_gather(gatherer, other, perm)
+    assert np.array_equal(got, other[oracle.argsort("u32", keys)])

@@ -56,6 +56,10 @@ def expected_argsort(kind, keys):
 
 def run_golden_case(c):
     kind = c["type"]
+    if c["op"] == "gather":
+        src = np.array(c["values"], dtype=BITS[kind])
+        got = oracle.gather(src, np.array(c["indices"], dtype=np.uint32))
+        return got.tolist() == c["expected_values"]
     keys = as_keys(kind, c["keys"])
     if c["op"] == "sort":
         got = oracle.sort(kind, keys)
@@ -160,6 +164,18 @@ def test_transform_closed_forms():
     assert np.array_equal(x[:-1] < x[1:], s[:-1] < s[1:])
 
 
+def test_gather_definition():
+    """gather = numpy fancy indexing; an index past the source is refused."""
+    g = np.random.Generator(np.random.PCG64(3))
+    for dt in (np.uint32, np.uint64):
+        src = g.integers(0, 1 << 63, size=5000, dtype=np.uint64).astype(dt)
+        idx = g.integers(0, 5000, size=20000, dtype=np.uint32)
+        assert np.array_equal(oracle.gather(src, idx), src[idx])
+        assert oracle.gather(src, np.zeros(0, dtype=np.uint32)).size == 0
+        with pytest.raises(IndexError):
+            oracle.gather(src, np.array([0, 5000], dtype=np.uint32))
+
+
 def test_edge_returns():
     assert oracle.sort("u32", np.array([], dtype=np.uint32)).size == 0
     assert oracle.argsort("f32", np.array([3.14], dtype=np.float32)).tolist() == [0]
@@ -184,6 +200,12 @@ def _all_checks_pass():
     for c in load_golden():
         if not run_golden_case(c):
             return False
+    g = np.random.Generator(np.random.PCG64(9))
+    for dt in (np.uint32, np.uint64):
+        src = g.integers(0, 1 << 32, size=1000, dtype=np.uint64).astype(dt)
+        idx = g.integers(0, 1000, size=3000, dtype=np.uint32)
+        if not np.array_equal(oracle.gather(src, idx), src[idx]):     # numpy fancy indexing
+            return False
     for kind in KINDS:
         keys = random_inputs(kind, 4097, seed=5)
         perm = expected_argsort(kind, keys)
@@ -194,7 +216,7 @@ def _all_checks_pass():
     return True
 
 
-@pytest.mark.parametrize("mutation", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("mutation", [1, 2, 3, 4, 5, 6])
 def test_planted_mistakes_are_caught(mutation):
     assert _all_checks_pass()
     oracle.set_mutation(mutation)
