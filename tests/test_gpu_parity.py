@@ -423,3 +423,64 @@ def test_sort_then_gather(sorter, gatherer):
     perm = sorter.argsort_u32(keys)
     got = gpu_gather(gatherer, other, perm)
     assert np.array_equal(got, other[oracle.argsort("u32", keys)])
+
+
+# ---- hipCUB DeviceRadixSort as an independent cross-check -----------------------
+
+@pytest.fixture(scope="module")
+def hipcub():
+    """tests/hipcub_xcheck/_build/libhipcub_xcheck.so (built by __graft_entry__.build())."""
+    import ctypes
+    path = os.path.join(os.path.dirname(__file__), "hipcub_xcheck", "_build", "libhipcub_xcheck.so")
+    assert os.path.exists(path), f"{path} not built: run __graft_entry__.build()"
+    L = ctypes.CDLL(path)
+    vp, u64 = ctypes.c_void_p, ctypes.c_uint64
+    fp = ctypes.POINTER(ctypes.c_float)
+    L.xc_sort_keys_u32.argtypes = [vp, vp, u64, fp]
+    L.xc_sort_keys_u64.argtypes = [vp, vp, u64, fp]
+    L.xc_sort_pairs_u32.argtypes = [vp, vp, vp, vp, u64, fp]
+    return L
+
+
+@pytest.mark.parametrize("kind,n", [("u32", 16_777_216), ("u32", 1_000_003), ("u64", 4_000_037)])
+def test_hipcub_crosscheck_keys(sorter, hipcub, kind, n):
+    """Keys sorted by this library and by hipCUB (ROCm's rocPRIM radix sort) are
+    identical, on device buffers."""
+    import ctypes
+    keys = make_keys(kind, n, "uniform", seed=700 + n)
+    a = sorter.alloc_sort_buffer(kind, n)
+    b = sorter.alloc_sort_buffer(kind, n)
+    a.copy_from_slice(keys)
+    ms = ctypes.c_float()
+    fn = hipcub.xc_sort_keys_u32 if kind == "u32" else hipcub.xc_sort_keys_u64
+    assert fn(ctypes.c_void_p(a.device_ptr()), ctypes.c_void_p(b.device_ptr()), n, ctypes.byref(ms)) == 0
+    sorter.sort_device(kind, a.device_ptr(), n)
+    a.set_len(n)
+    b.set_len(n)
+    ours, theirs = a.as_slice(), b.as_slice()
+    a.free()
+    b.free()
+    assert bits_equal(ours, theirs, kind), first_diff(ours, theirs, kind)
+    print(f"hipCUB SortKeys {kind} n={n}: {ms.value:.3f} ms")
+
+
+def test_hipcub_crosscheck_pairs(sorter, hipcub):
+    """Stable pairs: hipCUB's SortPairs order equals this library's (ties by
+    original position)."""
+    import ctypes
+    n = 5_000_011
+    keys = make_keys("u32", n, "few", seed=710)
+    vals = np.arange(n, dtype=np.uint32)
+    bufs = [sorter.alloc_sort_buffer("u32", n) for _ in range(4)]
+    bufs[0].copy_from_slice(keys)
+    bufs[2].copy_from_slice(vals)
+    ms = ctypes.c_float()
+    assert hipcub.xc_sort_pairs_u32(*[ctypes.c_void_p(b.device_ptr()) for b in (bufs[0], bufs[1], bufs[2], bufs[3])],
+                                    n, ctypes.byref(ms)) == 0
+    sorter.sort_pairs_device("u32", bufs[0].device_ptr(), bufs[2].device_ptr(), n)
+    out = []
+    for b in bufs:
+        b.set_len(n)
+        out.append(b.as_slice())
+        b.free()
+    assert np.array_equal(out[0], out[1]) and np.array_equal(out[2], out[3])
