@@ -22,6 +22,10 @@ imported, so the library runs on the ROCm HIP runtime it was built against
 rather than on the copy bundled with torch (both share one soname, and
 whichever loads first would serve both).
 
+Also reported, never as `value`: the slice API (sort_u32 on a 16M-key host
+array, host-to-device copy + sort + copy back, so PCIe-bound), as the
+reference's bench reports its slice and buffer APIs apart.
+
 Prints one JSON line.  --gpus > 1 is refused: this build measures one GPU.
 """
 import argparse
@@ -119,6 +123,7 @@ def main():
     ap.add_argument("--n", type=int, default=268_435_456)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-slice-api", action="store_true")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -200,6 +205,26 @@ def main():
                for k, v in sorted(by_kernel.items())}
     sort_frac = SORT_BYTES_PER_KEY * n / (ms_per_step / 1e3) / (HBM_PEAK_GBS * 1e9)
 
+    # The slice API (sort_u32 on a host array: copy in, sort, copy out), reported
+    # on its own as the reference's bench does; PCIe-bound, never `value`.
+    slice_api = None
+    if not args.no_slice_api:
+        ns = 16_777_216
+        host = datagen.uniform_u32(ns, seed=7)
+        work = host.copy()
+        sorter.sort_u32(work)                    # warm-up (grows the staging buffers)
+        runs = []
+        for _ in range(5):
+            work[:] = host
+            t0s = time.perf_counter()
+            sorter.sort_u32(work)
+            runs.append(time.perf_counter() - t0s)
+        ok_slice = bool(np.all(work[1:] >= work[:-1]))
+        slice_api = {"op": "sort_u32 (host slice: H2D + sort + D2H)", "n": ns,
+                     "value": round(ns / float(np.median(runs)) / 1e6, 1), "unit": "Mkeys/s",
+                     "ms": round(float(np.median(runs)) * 1e3, 3), "sorted": ok_slice}
+        del host, work
+
     cpu = None
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
@@ -217,6 +242,7 @@ def main():
         "sort_roofline": {"bytes_per_key": SORT_BYTES_PER_KEY, "frac": round(sort_frac, 4),
                           "achieved_GBps": round(sort_frac * HBM_PEAK_GBS, 1)},
         "kernels": kernels, "kernel_ms_per_step": round(kernel_sum_ms, 4),
+        "slice_api": slice_api,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

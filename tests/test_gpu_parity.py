@@ -484,3 +484,65 @@ def test_hipcub_crosscheck_pairs(sorter, hipcub):
         out.append(b.as_slice())
         b.free()
     assert np.array_equal(out[0], out[1]) and np.array_equal(out[2], out[3])
+
+
+# ---- caller streams (with_context, encode on a given stream) ---------------------
+
+@pytest.fixture(scope="module")
+def hip_stream():
+    """A HIP stream of the caller, created through the HIP runtime the library
+    itself is linked against."""
+    import ctypes
+    import forge_sort
+    forge_sort._load()                                   # libamdhip64 is loaded with it
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    st = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(st)) == 0
+    yield st.value
+    hip.hipStreamSynchronize(st)
+    hip.hipStreamDestroy(st)
+
+
+def test_with_context_caller_stream(hip_stream):
+    """GpuSorter::with_context on the caller's stream (lib.rs:606-686): every op
+    and the async encode run there; results match the oracle."""
+    from forge_sort import OP_ARGSORT, OP_PAIRS, GpuSorter
+    s = GpuSorter.with_context(0, hip_stream)
+    try:
+        keys = make_keys("f32", 500_001, "uniform", seed=801)
+        got = keys.copy()
+        s.sort_f32(got)
+        assert bits_equal(got, oracle.sort("f32", keys), "f32")
+        k64 = make_keys("i64", 300_007, "few", seed=802)
+        assert np.array_equal(s.argsort_i64(k64), oracle.argsort("i64", k64))
+        # encode on the caller stream, then wait for it through the sorter
+        n = 1_000_003
+        keys = make_keys("u32", n, "uniform", seed=803)
+        vals = np.arange(n, dtype=np.uint32)
+        kb, vb, ib = (s.alloc_sort_buffer("u32", n) for _ in range(3))
+        kb.copy_from_slice(keys)
+        vb.copy_from_slice(vals)
+        s.encode(OP_PAIRS, "u32", kb.device_ptr(), vb.device_ptr(), n, stream=hip_stream)
+        s.synchronize()
+        ek, ev = oracle.sort_pairs("u32", keys, vals)
+        assert np.array_equal(kb.as_slice(), ek) and np.array_equal(vb.as_slice(), ev)
+        kb.copy_from_slice(keys)
+        s.encode(OP_ARGSORT, "u32", kb.device_ptr(), ib.device_ptr(), n, stream=hip_stream)
+        s.synchronize()
+        ib.set_len(n)
+        assert np.array_equal(ib.as_slice(), oracle.argsort("u32", keys))
+        for b in (kb, vb, ib):
+            b.free()
+    finally:
+        s.close()
+
+
+def test_gather_with_context_caller_stream(hip_stream):
+    from forge_sort import GpuGather
+    g = GpuGather.with_context(0, hip_stream)
+    try:
+        src = np.arange(1000, dtype=np.uint64) * 3
+        idx = np.random.Generator(np.random.PCG64(5)).integers(0, 1000, size=5000, dtype=np.uint32)
+        assert np.array_equal(gpu_gather(g, src, idx), src[idx])
+    finally:
+        g.close()
