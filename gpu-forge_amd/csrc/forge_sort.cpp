@@ -312,8 +312,10 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         void* args2[] = {&a, &digit};
         if ((r = launch(s, os, num_tiles, s->block[var], args2, st)) != FS_OK) return r;
     }
+    // fs_finish mostly finds nothing to do (every schedule but a single
+    // in-place pass ends in the caller's buffers): a small grid exits fast.
     uint64_t fin_blocks = (n + 255) / 256;
-    if (fin_blocks > (uint64_t)s->num_cus * 8) fin_blocks = (uint64_t)s->num_cus * 8;
+    if (fin_blocks > (uint64_t)s->num_cus * 2) fin_blocks = (uint64_t)s->num_cus * 2;
     if ((r = launch(s, K_FINISH, (unsigned)fin_blocks, 256, args1, st)) != FS_OK) return r;
     s->last_stream = st;
     s->pending = true;

@@ -43,8 +43,11 @@
 #define FS_VAR_K64 2
 #define FS_VAR_K64V 3
 
-// Upsweep (all-digit histogram) block.
+// Upsweep (all-digit histogram) block, and 16-byte loads in flight per lane.
 #define FS_HIST_BLOCK 256
+#ifndef FS_UPSWEEP_UNROLL
+#define FS_UPSWEEP_UNROLL 4
+#endif
 
 // Look-back tile entries, one per (tile, digit), in a single chain over all
 // tiles: a 32-bit word [flag:2 | value:30] when n < FS_LB_WIDE_KEYS, else a
