@@ -60,7 +60,6 @@ struct fs_sorter {
     DevBuf s1k, s2k, s1v, s2v, lb0, lb1, iok, iov;
     uint32_t* hist = nullptr;       // [8][256], zero between sorts
     uint32_t* binbase = nullptr;    // [8][256]
-    uint32_t* tile_ctr = nullptr;   // [8]
     uint32_t* plan = nullptr;       // u32[FS_PLAN_WORDS] device-side schedule
     uint32_t* status = nullptr;     // pinned host word written by kernels on device errors
     unsigned long long* stats = nullptr;   // device u64[FS_STAT_COUNT]
@@ -297,7 +296,6 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.binbase = (uint64_t)(uintptr_t)s->binbase;
     a.lookback0 = (uint64_t)(uintptr_t)s->lb0.p;
     a.lookback1 = (uint64_t)(uintptr_t)s->lb1.p;
-    a.tile_ctr = (uint64_t)(uintptr_t)s->tile_ctr;
     a.plan = (uint64_t)(uintptr_t)s->plan;
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
@@ -424,14 +422,13 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
     }
     const size_t tab = (size_t)FS_MAX_DIGITS * FS_RADIX * 4;
     if (hipMalloc(&s->hist, tab) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||
-        hipMalloc(&s->tile_ctr, FS_MAX_DIGITS * 4) != hipSuccess ||
         hipMalloc(&s->plan, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc(&s->stats, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
         return create_failed(s, FS_ERR_OUT_OF_MEMORY, "device tables of the sorter");
     *s->status = 0;
     // The histogram table must start at zero; fs_plan re-zeroes it after every sort.
-    if (hipMemset(s->hist, 0, tab) != hipSuccess || hipMemset(s->tile_ctr, 0, FS_MAX_DIGITS * 4) != hipSuccess ||
+    if (hipMemset(s->hist, 0, tab) != hipSuccess ||
         hipMemset(s->stats, 0, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipMemset(s->plan, 0, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess)
@@ -457,7 +454,6 @@ void fs_sorter_free(fs_sorter* s) {
     for (DevBuf* b : bufs) free_buf(*b);
     if (s->hist) (void)hipFree(s->hist);
     if (s->binbase) (void)hipFree(s->binbase);
-    if (s->tile_ctr) (void)hipFree(s->tile_ctr);
     if (s->plan) (void)hipFree(s->plan);
     if (s->stats) (void)hipFree(s->stats);
     if (s->status) (void)hipHostFree(s->status);

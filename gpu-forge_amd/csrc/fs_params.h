@@ -62,6 +62,15 @@
 #define FS_LB_WIDE_KEYS (1u << 30)
 #endif
 
+// XCDs of the device and consecutive tiles given to one XCD by a digit pass's
+// block-to-tile mapping.
+#ifndef FS_XCDS
+#define FS_XCDS 8
+#endif
+#ifndef FS_XCD_TILES
+#define FS_XCD_TILES 4
+#endif
+
 // Predecessor tile entries read per look-back round trip.
 #ifndef FS_LB_WINDOW
 #define FS_LB_WINDOW 4
@@ -128,7 +137,7 @@
 #define FS_PLAN_WORDS (FS_PLAN_NPASSES + 4)
 
 // Error bits additionally reported through the status word.
-#define FS_DEVERR_BAD_TILE 2u        // a digit pass drew a tile id >= num_tiles
+#define FS_DEVERR_BAD_TILE 2u        // a digit pass block mapped to a tile >= num_tiles
 #define FS_DEVERR_BAD_PLAN 4u        // a schedule named a buffer the call does not have
 #define FS_DEVERR_GATHER_INDEX 8u    // a gather index was >= the source length
 
@@ -152,7 +161,6 @@ typedef struct FsArgs {
     uint64_t binbase;           // u32 [digits][256]
     uint64_t lookback0, lookback1;  // [num_tiles][256] tile entries (u32, or u64 when wide),
                                     // then u32 [groups][256] group entries; alternate per pass
-    uint64_t tile_ctr;          // u32 [FS_MAX_DIGITS]
     uint64_t plan;              // u32[FS_PLAN_WORDS] schedule
     uint64_t status;            // u32, host-visible error bits
     uint64_t stats;             // u64[FS_STAT_SLOTS][FS_STAT_COUNT] look-back counters, or 0 when off

@@ -2,9 +2,12 @@
 // host runtime use (TEST INFRASTRUCTURE ONLY; see hip/hip_runtime.h).
 //
 // Execution model:
-//  * a launch runs its blocks on a pool of OS threads (EMU_WORKERS, default 4),
-//    handed out in increasing block order, so several blocks are resident at
-//    once and the look-back between tiles is a real cross-thread race;
+//  * a launch runs its blocks on a pool of OS threads, several blocks resident
+//    at once so that the look-back between tiles is a real cross-thread race.
+//    As on the device, blocks are dealt round-robin to EMU_XCDS queues (default
+//    8, block b to queue b % EMU_XCDS) and every queue starts its blocks in
+//    increasing order; EMU_WORKERS threads (default 8, rounded up to a
+//    multiple of the queues) serve the queues;
 //  * inside a block every GPU thread is a ucontext fiber, scheduled round-robin;
 //  * __syncthreads waits for every live thread of the block;
 //  * a wave64 operation completes once no lane of the wave is still runnable:
@@ -235,17 +238,27 @@ static void run_block(uint32_t bid, uint32_t grid, uint32_t nthreads, void (*ent
     B = nullptr;
 }
 
+static int xcds() {
+    const char* e = getenv("EMU_XCDS");
+    int x = e ? atoi(e) : 8;
+    return x > 0 ? x : 1;
+}
+
 static int workers() {
     const char* e = getenv("EMU_WORKERS");
-    int w = e ? atoi(e) : 4;
-    return w > 0 ? w : 1;
+    int w = e ? atoi(e) : 8;
+    const int x = xcds();
+    if (w < x) w = x;
+    return (w + x - 1) / x * x;
 }
 
 void launch(const char* name, void (*entry)(void**), uint32_t grid, uint32_t block, void** params) {
     g_kernel = name;
     if (getenv("EMU_TRACE")) fprintf(stderr, "hip_emu: launch %s grid=%u block=%u\n", name, grid, block);
-    std::atomic<uint32_t> next{0};
-    auto worker = [&]() {
+    const int nx = xcds();
+    std::vector<std::atomic<uint32_t>> next(nx);           // per-queue position
+    for (auto& c : next) c = 0;
+    auto worker = [&](int queue) {
         if (!getenv("EMU_NO_SEGV_HANDLER")) {
             stack_t ss;                   // the signal handler's stack; kept for the process
             ss.ss_size = 1 << 16;
@@ -254,14 +267,14 @@ void launch(const char* name, void (*entry)(void**), uint32_t grid, uint32_t blo
             sigaltstack(&ss, nullptr);
         }
         for (;;) {
-            const uint32_t b = next.fetch_add(1);
+            const uint64_t b = (uint64_t)queue + (uint64_t)nx * next[queue].fetch_add(1);
             if (b >= grid) break;
-            run_block(b, grid, block, entry, params);
+            run_block((uint32_t)b, grid, block, entry, params);
         }
     };
     std::vector<std::thread> pool;
-    const int nw = std::min<int>(workers(), (int)grid);
-    for (int i = 0; i < nw; ++i) pool.emplace_back(worker);
+    const int nw = workers();
+    for (int i = 0; i < nw; ++i) pool.emplace_back(worker, i % nx);
     for (auto& t : pool) t.join();
 }
 

@@ -104,3 +104,11 @@ def test_emulated_upsweep_long_segments(emulator):
              "offset:f32:3:uniform:7"]
     for flavor in ("small", "prod"):
         run_cases(flavor, cases, env={"EMU_CUS": "1", "FS_UPSWEEP_BLOCKS_PER_CU": "1"})
+
+
+def test_emulated_single_dispatch_queue(emulator):
+    """Blocks started in plain increasing order from one queue (not dealt over
+    XCDs), 40 at a time: a digit-pass tile then may wait on a tile whose block
+    starts up to 31 blocks later, which the resident blocks allow."""
+    run_cases("small", ["sort:u32:70000:uniform:2", "pairs:u32:40000:uniform:7", "sort:u64:9000:uniform:3"],
+              env={"EMU_XCDS": "1", "EMU_WORKERS": "40"})
