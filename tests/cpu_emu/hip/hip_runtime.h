@@ -73,6 +73,28 @@ inline int32_t emu_sbfe(int32_t x, int off, int width) {
     if (width < 32 && (u >> (width - 1)) & 1u) u |= ~((1u << width) - 1u);
     return (int32_t)u;
 }
+// v_bfe_u32: offset and width are taken from their low 5 bits.
+inline uint32_t emu_ubfe(uint32_t x, uint32_t off, uint32_t width) {
+    off &= 31u; width &= 31u;
+    if (width == 0) return 0u;
+    return (x >> off) & ((1u << width) - 1u);
+}
+// v_perm_b32: result byte i is chosen by selector byte i from the bytes of
+// {src0, src1} (0-3: src1, 4-7: src0), 8-11 sign bits, 12 = 0x00, >= 13 = 0xFF.
+inline uint32_t emu_perm(uint32_t src0, uint32_t src1, uint32_t sel) {
+    const uint64_t v = ((uint64_t)src0 << 32) | src1;
+    uint32_t r = 0;
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t s = (sel >> (8 * i)) & 0xFFu;
+        uint32_t b;
+        if (s < 8u) b = (uint32_t)(v >> (8 * s)) & 0xFFu;
+        else if (s < 12u) b = ((v >> (16 * (s - 8u) + 15)) & 1u) ? 0xFFu : 0x00u;
+        else if (s == 12u) b = 0x00u;
+        else b = 0xFFu;
+        r |= b << (8 * i);
+    }
+    return r;
+}
 inline uint32_t emu_bitop3(uint32_t a, uint32_t b, uint32_t c, uint32_t tt) {
     uint32_t r = 0;
     for (int i = 0; i < 8; ++i) {
@@ -95,6 +117,8 @@ inline uint32_t emu_mbcnt_hi(uint32_t mask, uint32_t acc) {
 #define __builtin_amdgcn_readfirstlane(v) emu_readfirstlane((uint32_t)(v))
 #define __builtin_amdgcn_uicmp(a, b, p) emu_uicmp((uint32_t)(a), (uint32_t)(b), (p))
 #define __builtin_amdgcn_sbfe(x, o, w) emu_sbfe((int32_t)(x), (o), (w))
+#define __builtin_amdgcn_ubfe(x, o, w) emu_ubfe((uint32_t)(x), (o), (w))
+#define __builtin_amdgcn_perm(a, b, s) emu_perm((uint32_t)(a), (uint32_t)(b), (uint32_t)(s))
 #define __builtin_amdgcn_bitop3_b32(a, b, c, t) emu_bitop3((a), (b), (c), (t))
 #define __builtin_amdgcn_mbcnt_lo(m, a) emu_mbcnt_lo((m), (a))
 #define __builtin_amdgcn_mbcnt_hi(m, a) emu_mbcnt_hi((m), (a))
