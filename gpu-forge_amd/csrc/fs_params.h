@@ -43,6 +43,12 @@
 #define FS_VAR_K64 2
 #define FS_VAR_K64V 3
 
+// Histogram atomics: a wave whose lanes share one digit with at least
+// FS_PEEL_MIN others adds that digit's lanes with one atomic.
+#ifndef FS_PEEL_MIN
+#define FS_PEEL_MIN 8
+#endif
+
 // Upsweep (all-digit histogram) block, and 16-byte loads in flight per lane.
 #define FS_HIST_BLOCK 256
 #ifndef FS_UPSWEEP_UNROLL

@@ -41,6 +41,10 @@ def keys_for(kind, n, dist, seed):
         b = np.full(n, 7, dtype=BITS[kind])
     elif dist == "low12":
         b = g.integers(0, 1 << 12, size=n, dtype=BITS[kind])
+    elif dist == "zipf":
+        # a dominant bin: Zipf(1.1) ranks below 2^20 (most keys small, digit 1
+        # and 2 mostly zero), as in the pairs benchmark config
+        b = np.minimum(g.zipf(1.1, size=n) - 1, (1 << 20) - 1).astype(BITS[kind])
     else:
         raise ValueError(dist)
     return b.view(oracle.NP_DTYPES[kind])

@@ -57,12 +57,15 @@ SMALL_CASES = [
     "argsort:f64:1025:uniform:25",
     # GpuGather
     "gather:u32:5000:uniform:26", "gather:u64:3001:uniform:27",
+    # dominant bins: histogram atomics of the shared digit added once per wave
+    "sort:u32:9000:zipf:28", "pairs:u32:7000:zipf:29", "argsort:u64:3000:zipf:30",
 ]
 
 PROD_CASES = [
     "sort:u32:40000:uniform:1", "sort:u32:12289:uniform:2", "argsort:f32:30000:few:3",
     "pairs:u64:20000:uniform:4", "sort:i64:20000:low12:6", "pairs:u32:25000:few:7",
     "sort:f64:9000:uniform:8", "argsort:i32:13000:uniform:9",
+    "pairs:u32:30000:zipf:10", "sort:u32:26000:few:11",
 ]
 
 
