@@ -27,6 +27,11 @@ array, host-to-device copy + sort + copy back, so PCIe-bound), as the
 reference's bench reports its slice and buffer APIs apart.
 
 Prints one JSON line.  --gpus > 1 is refused: this build measures one GPU.
+
+--workload picks one of the other BASELINE.json configs (64-bit keys, floats,
+argsort, pairs, the 1M and 16M sizes) for the same measurement: its own metric
+line with the roofline of its dominant digit-pass kernel, no CPU baseline and
+no slice API.  The default (no flag) is the headline line above.
 """
 import argparse
 import ctypes
@@ -47,6 +52,85 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 PASS_BYTES_PER_KEY = 8         # one read + one write of a u32 key per digit pass
 SORT_BYTES_PER_KEY = 36        # k + k*2*k for k = 4 (histogram read + 4 passes)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "onesweep_k32_u32_256M_traffic.json")
+
+
+# name -> (op, key type, n, data description, BASELINE.json config)
+WORKLOADS = {
+    "u32_256M": ("sort", "u32", 268_435_456, "uniform u32 over [0, 2^32), numpy PCG64 seed 2024", "configs[1]"),
+    "u32_16M": ("sort", "u32", 16_777_216, "uniform u32 over [0, 2^32), numpy PCG64 seed 2024", "configs[1]"),
+    "u32_1M": ("sort", "u32", 1_048_576, "uniform u32 over [0, 2^32), numpy PCG64 seed 2024", "configs[0]"),
+    "f32_64M": ("sort", "f32", 67_108_864, "98% N(0, 1e3), 2% -0.0/+0.0/+-inf/subnormals/NaN, seed 5", "configs[2]"),
+    "i32_64M": ("sort", "i32", 67_108_864, "uniform over the full i32 range, seed 2", "configs[2]"),
+    "argsort_f32_16M": ("argsort", "f32", 16_777_216, "uniform [-1, 1) quantised to 4096 values, seed 6", "configs[3]"),
+    "pairs_u32_64M": ("pairs", "u32", 67_108_864, "Zipf(1.1) keys below 2^20 with a 10% run of one key, values = index, seed 7", "configs[3]"),
+    "u64_128M": ("sort", "u64", 134_217_728, "uniform u64, seed 3", "configs[4]"),
+    "i64_128M": ("sort", "i64", 134_217_728, "uniform i64, seed 4", "configs[4]"),
+    "f64_128M": ("sort", "f64", 134_217_728, "N(0, 1e6), seed 8", "configs[4]"),
+    "u64_low20_128M": ("sort", "u64", 134_217_728, "high 44 bits 0, low 20 bits uniform, seed 9", "configs[4]"),
+}
+
+
+def workload_input(name, n):
+    """Keys (and values for pairs) of a workload, from the seeded generators."""
+    from forge_sort import datagen
+    kind = WORKLOADS[name][1]
+    if name.startswith("u32"):
+        return datagen.uniform_u32(n, seed=2024), None
+    if name == "f32_64M":
+        return datagen.f32_normal_specials(n, 5), None
+    if name == "i32_64M":
+        return datagen.uniform_i32(n, 2), None
+    if name == "argsort_f32_16M":
+        return datagen.argsort_f32_ties(n, 6), None
+    if name == "pairs_u32_64M":
+        return datagen.zipf_pairs_u32(n, 7)
+    if name == "u64_128M":
+        return datagen.uniform_u64(n, 3), None
+    if name == "i64_128M":
+        return datagen.uniform_i64(n, 4), None
+    if name == "f64_128M":
+        return datagen.normal_f64(n, 8), None
+    if name == "u64_low20_128M":
+        return datagen.low20_u64(n, 0, 9), None
+    raise ValueError(kind)
+
+
+def ordered_bits(a):
+    """Keys as unsigned integers in the sort's order: sign flip for signed
+    types, FloatFlip (IEEE total order) for floats."""
+    w = a.dtype.itemsize * 8
+    u = a.view(np.uint32 if w == 32 else np.uint64)
+    top = (np.uint32 if w == 32 else np.uint64)(1 << (w - 1))
+    if a.dtype.kind == "i":
+        return u ^ top
+    if a.dtype.kind == "f":
+        neg = (u >> (w - 1)).astype(bool)
+        return np.where(neg, ~u, u ^ top)
+    return u
+
+
+def check_output(op, keys_in, vals_in, keys_out, vals_out):
+    """Sorted in the key order, same multiset; argsort/pairs: stable (ties by
+    original index, values being the original index for the pairs input)."""
+    ok = True
+    if op == "argsort":
+        idx = vals_out.astype(np.int64)
+        ok &= bool(np.array_equal(np.sort(idx), np.arange(idx.size)))
+        o = ordered_bits(keys_in[idx])
+    else:
+        o = ordered_bits(keys_out)
+        u_in = keys_in.view(o.dtype)
+        u_out = keys_out.view(o.dtype)
+        ok &= int(u_in.astype(np.uint64).sum()) == int(u_out.astype(np.uint64).sum())
+        ok &= int(np.bitwise_xor.reduce(u_in)) == int(np.bitwise_xor.reduce(u_out))
+        idx = vals_out.astype(np.int64) if op == "pairs" else None
+        if op == "pairs":
+            ok &= bool(np.array_equal(keys_in[idx], keys_out))
+    ok &= bool(np.all(o[1:] >= o[:-1]))
+    if idx is not None:
+        tie = o[1:] == o[:-1]
+        ok &= bool(np.all(idx[1:][tie] > idx[:-1][tie]))
+    return ok
 
 
 def log(*a):
@@ -120,7 +204,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--n", type=int, default=268_435_456)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="u32_256M")
+    ap.add_argument("--n", type=int, default=None, help="override the workload's key count")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-slice-api", action="store_true")
@@ -131,27 +216,45 @@ def main():
               "single-GPU and no multi-GPU path is built", file=sys.stderr)
         sys.exit(2)
 
-    from forge_sort import OP_SORT, DeviceNotFound, GpuSorter, datagen
+    from forge_sort import OP_ARGSORT, OP_PAIRS, OP_SORT, DeviceNotFound, GpuSorter, datagen
     try:
         sorter = GpuSorter.new(0)
     except DeviceNotFound:
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
 
-    n, K, W = args.n, args.steps, args.warmup
-    log(f"bench: sort_buffer u32 n={n:,} steps={K} warmup={W}")
-    keys = datagen.uniform_u32(n, seed=2024)
-    src = sorter.alloc_sort_buffer("u32", n)
+    wl = args.workload
+    headline = wl == "u32_256M"
+    op_name, kind, n_default, data_desc, cfg_ref = WORKLOADS[wl]
+    n = args.n or n_default
+    K, W = args.steps, args.warmup
+    op = {"sort": OP_SORT, "argsort": OP_ARGSORT, "pairs": OP_PAIRS}[op_name]
+    log(f"bench: {wl} ({op_name} {kind}) n={n:,} steps={K} warmup={W}")
+    keys, vals = workload_input(wl, n)
+    ksize = keys.dtype.itemsize
+    src = sorter.alloc_sort_buffer(kind, n)
     src.copy_from_slice(keys)
-    bufs = []
+    vsrc = None
+    if op == OP_PAIRS:
+        vsrc = sorter.alloc_sort_buffer("u32", n)
+        vsrc.copy_from_slice(vals)
+    bufs, vbufs = [], []
     for _ in range(W + K):
-        b = sorter.alloc_sort_buffer("u32", n)
-        sorter.copy_device(b.device_ptr(), src.device_ptr(), 4 * n)
+        b = sorter.alloc_sort_buffer(kind, n)
+        sorter.copy_device(b.device_ptr(), src.device_ptr(), ksize * n)
         bufs.append(b)
+        if op != OP_SORT:
+            v = sorter.alloc_sort_buffer("u32", n)
+            if op == OP_PAIRS:
+                sorter.copy_device(v.device_ptr(), vsrc.device_ptr(), 4 * n)
+            vbufs.append(v)
     sorter.device_synchronize()
 
+    def vptr(i):
+        return vbufs[i].device_ptr() if vbufs else None
+
     for i in range(W):
-        sorter.encode(OP_SORT, "u32", bufs[i].device_ptr(), None, n)
+        sorter.encode(op, kind, bufs[i].device_ptr(), vptr(i), n)
     sorter.synchronize()
 
     sorter.set_profiling(True)
@@ -159,56 +262,70 @@ def main():
     sorter.device_synchronize()
     t0 = time.perf_counter()
     for i in range(K):
-        sorter.encode(OP_SORT, "u32", bufs[W + i].device_ptr(), None, n)
+        sorter.encode(op, kind, bufs[W + i].device_ptr(), vptr(W + i), n)
     sorter.synchronize()
     sorter.device_synchronize()
     t1 = time.perf_counter()
     prof = sorter.profile()
     sorter.set_profiling(False)
+    _, digit_mask = sorter.last_pass_info()      # digits whose pass ran (same input every step)
     log(f"bench: timed {K} sorts in {t1 - t0:.4f} s")
 
-    # sanity: the last output is sorted and holds the same multiset (checksums)
+    # the last output: sorted, same multiset, stable for argsort and pairs
     bufs[-1].set_len(n)
-    last = bufs[-1].as_slice()
-    ok_sorted = bool(np.all(last[1:] >= last[:-1]))
-    ok_sum = int(last.astype(np.uint64).sum()) == int(keys.astype(np.uint64).sum())
-    ok_xor = int(np.bitwise_xor.reduce(last)) == int(np.bitwise_xor.reduce(keys))
-    del last
-    for b in bufs:
+    keys_out = bufs[-1].as_slice()
+    vals_out = None
+    if vbufs:
+        vbufs[-1].set_len(n)
+        vals_out = vbufs[-1].as_slice()
+    ok = check_output(op_name, keys, vals, keys_out, vals_out)
+    del keys_out, vals_out
+    for b in bufs + vbufs:
         b.free()
     src.free()
-    if not (ok_sorted and ok_sum and ok_xor):
+    if vsrc is not None:
+        vsrc.free()
+    if not ok:
         print("bench: output check FAILED", file=sys.stderr)
         sys.exit(3)
 
     ms_per_step = (t1 - t0) * 1e3 / K
     value = n / (ms_per_step / 1e3) / 1e6
 
+    # Digit-pass kernel and algorithmic bytes (one read + one write of every
+    # key and value per pass; whole sort B(k,v) = k + 2k(k+v) per key).
+    vbytes = 4 if op != OP_SORT else 0
+    pass_kernel = "fs_onesweep_" + ("k64" if ksize == 8 else "k32") + ("_v" if vbytes else "")
+    pass_bytes = 2 * (ksize + vbytes)
+    sort_bytes = ksize + 2 * ksize * (ksize + vbytes)
     by_kernel = {}
     for name, ms in prof:
         by_kernel.setdefault(name, []).append(ms)
-    passes = by_kernel.get("fs_onesweep_k32", [])
-    active = [ms for ms in passes if ms > 0.02]      # constant-digit launches exit at once
+    # every sort launches one digit pass per digit position, in digit order; a
+    # constant digit's launch exits at once and is not averaged
+    digits = ksize                                 # 8-bit digits: one per key byte
+    passes = by_kernel.get(pass_kernel, [])
+    active = [ms for i, ms in enumerate(passes) if digit_mask >> (i % digits) & 1]
     pass_ms = float(np.mean(active)) if active else float("nan")
-    achieved = PASS_BYTES_PER_KEY * n / (pass_ms / 1e3) / 1e9
+    achieved = pass_bytes * n / (pass_ms / 1e3) / 1e9
     kernel_sum_ms = sum(ms for _, ms in prof) / K
-    traffic = load_traffic()
+    traffic = load_traffic() if headline else None
     roofline = {
-        "bound": "hbm", "kernel": "fs_onesweep_k32",
+        "bound": "hbm", "kernel": pass_kernel,
         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic.get("bytes_per_launch") if traffic else None,
-        "bytes_per_launch_algorithmic": PASS_BYTES_PER_KEY * n,
+        "bytes_per_launch_algorithmic": pass_bytes * n,
         "avg_launch_ms": round(pass_ms, 4), "launches": len(active),
     }
     kernels = {k: {"avg_ms": round(float(np.mean(v)), 4), "launches": len(v)}
                for k, v in sorted(by_kernel.items())}
-    sort_frac = SORT_BYTES_PER_KEY * n / (ms_per_step / 1e3) / (HBM_PEAK_GBS * 1e9)
+    sort_frac = sort_bytes * n / (ms_per_step / 1e3) / (HBM_PEAK_GBS * 1e9)
 
     # The slice API (sort_u32 on a host array: copy in, sort, copy out), reported
     # on its own as the reference's bench does; PCIe-bound, never `value`.
     slice_api = None
-    if not args.no_slice_api:
+    if headline and not args.no_slice_api:
         ns = 16_777_216
         host = datagen.uniform_u32(ns, seed=7)
         work = host.copy()
@@ -226,20 +343,25 @@ def main():
         del host, work
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if headline and not args.no_cpu_baseline:
         log("bench: cpu baseline")
         cpu = cpu_baseline(keys, args.cpu_seconds)
 
+    api = {"sort": "sort_buffer", "argsort": "argsort (device buffers)",
+           "pairs": "sort_pairs (device buffers)"}[op_name]
+    if headline and n == n_default:
+        workload = "sort_buffer u32, 268,435,456 keys, device resident (BASELINE.json configs[1])"
+    else:
+        workload = f"{api} {kind}, {n:,} keys, device resident (BASELINE.json {cfg_ref})"
     line = {
-        "metric": METRIC, "value": round(value, 1), "unit": "Mkeys/s", "n_gpus": 1,
+        "metric": METRIC if headline else f"Mkeys/s ({wl}, 1 MI355X) and % of HBM-bandwidth roofline",
+        "value": round(value, 1), "unit": "Mkeys/s", "n_gpus": 1,
         "steps": K, "warmup": W, "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32",
-        "data": "synthetic: uniform u32 over [0, 2^32), numpy PCG64 seed 2024, resident in HBM",
-        "config": {"workload": "sort_buffer u32, 268,435,456 keys, device resident (BASELINE.json configs[1])"
-                   if n == 268_435_456 else f"sort_buffer u32, {n:,} keys, device resident",
-                   "n": n, "key_type": "u32", "op": "sort_buffer"},
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": kind,
+        "data": f"synthetic: {data_desc}, resident in HBM",
+        "config": {"workload": workload, "n": n, "key_type": kind, "op": api},
         "roofline": roofline,
-        "sort_roofline": {"bytes_per_key": SORT_BYTES_PER_KEY, "frac": round(sort_frac, 4),
+        "sort_roofline": {"bytes_per_key": sort_bytes, "frac": round(sort_frac, 4),
                           "achieved_GBps": round(sort_frac * HBM_PEAK_GBS, 1)},
         "kernels": kernels, "kernel_ms_per_step": round(kernel_sum_ms, 4),
         "slice_api": slice_api,
