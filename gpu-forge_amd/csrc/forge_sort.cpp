@@ -6,7 +6,7 @@
 // :1520-1639, encode_sort_pipeline_64 :1302-1478) with HIP: one device, one
 // stream, the gfx950 code object loaded by hipModuleLoad, grow-only scratch
 // in HBM, and a fixed launch sequence per sort:
-//   fs_upsweep -> fs_plan -> fs_onesweep x digits -> fs_finish
+//   fs_upsweep (its last block writes the schedule) -> fs_onesweep x digits -> fs_finish
 // The sequence never reads anything back to the host, so fs_encode is fully
 // asynchronous; which digit passes really run is decided on the device.
 //
@@ -38,11 +38,11 @@ struct ProfEntry {
 };
 
 const char* const kKernelNames[] = {
-    "fs_upsweep_k32", "fs_upsweep_k64", "fs_plan",   "fs_onesweep_k32", "fs_onesweep_k32_v",
+    "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_finish", "fs_iota",
 };
 enum {
-    K_UP32, K_UP64, K_PLAN, K_OS32, K_OS32V, K_OS64, K_OS64V, K_FINISH, K_IOTA, K_COUNT
+    K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_FINISH, K_IOTA, K_COUNT
 };
 
 }  // namespace
@@ -303,7 +303,6 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     const unsigned up_grid = (num_tiles + tpb - 1) / tpb;
     void* args1[] = {&a};
     if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st)) != FS_OK) return r;
-    if ((r = launch(s, K_PLAN, 1, FS_RADIX, args1, st)) != FS_OK) return r;
     const int os = K_OS32 + var;   // kernel order matches FS_VAR_*
     for (uint32_t d = 0; d < a.digits; ++d) {
         uint32_t digit = d;
@@ -427,7 +426,8 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
         hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
         return create_failed(s, FS_ERR_OUT_OF_MEMORY, "device tables of the sorter");
     *s->status = 0;
-    // The histogram table must start at zero; fs_plan re-zeroes it after every sort.
+    // The histogram table and the upsweep's ticket must start at zero; the
+    // upsweep's last block re-zeroes both after every sort.
     if (hipMemset(s->hist, 0, tab) != hipSuccess ||
         hipMemset(s->stats, 0, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipMemset(s->plan, 0, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||

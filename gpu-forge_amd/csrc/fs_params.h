@@ -122,7 +122,7 @@
 // Error bits reported through the host-visible status word.
 #define FS_DEVERR_LOOKBACK_TIMEOUT 1u
 
-// Device-side schedule written by fs_plan: FS_PLAN_WORDS u32 words, stored
+// Device-side schedule written by the upsweep's last block: FS_PLAN_WORDS u32 words, stored
 // and loaded with agent-scope (sc1) accesses.  Buffers are named by id, never
 // by address, so a kernel only ever dereferences addresses from its own
 // arguments.
@@ -140,7 +140,8 @@
 #define FS_PLAN_FINISH (FS_PLAN_NPASSES + 1)                       // FS_FIN_*
 #define FS_PLAN_MASK (FS_PLAN_NPASSES + 2)                         // bit j: digit j sorted
 #define FS_PLAN_FINBUF (FS_PLAN_NPASSES + 3)                       // finish buffer ids, as word 2j+1
-#define FS_PLAN_WORDS (FS_PLAN_NPASSES + 4)
+#define FS_PLAN_TICKET (FS_PLAN_NPASSES + 4)                       // upsweep blocks finished (0 between sorts)
+#define FS_PLAN_WORDS (FS_PLAN_NPASSES + 5)
 
 // Error bits additionally reported through the status word.
 #define FS_DEVERR_BAD_TILE 2u        // a digit pass block mapped to a tile >= num_tiles

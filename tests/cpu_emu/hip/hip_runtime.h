@@ -47,6 +47,9 @@ unsigned lane();
 
 inline void __syncthreads() { emu::syncthreads(); }
 inline int __syncthreads_or(int p) { return emu::syncthreads_or(p); }
+inline void __threadfence() { __atomic_thread_fence(__ATOMIC_SEQ_CST); }
+// every emulated memory operation has completed when the lane continues
+#define __builtin_amdgcn_s_waitcnt(imm) __atomic_thread_fence(__ATOMIC_SEQ_CST)
 inline unsigned long long __ballot(int p) { return emu::ballot(p); }
 inline int __all(int p) { return emu::all(p); }
 inline uint32_t __shfl_up(uint32_t v, unsigned off, int /*width*/) { return emu::shfl_up(v, off); }
@@ -140,6 +143,7 @@ inline uint32_t atomicAdd(uint32_t* p, uint32_t v) { return __atomic_fetch_add(p
 inline unsigned long long atomicAdd(unsigned long long* p, unsigned long long v) {
     return __atomic_fetch_add(p, v, __ATOMIC_ACQ_REL);
 }
+inline uint32_t atomicOr(uint32_t* p, uint32_t v) { return __atomic_fetch_or(p, v, __ATOMIC_ACQ_REL); }
 inline unsigned long long atomicOr(unsigned long long* p, unsigned long long v) {
     return __atomic_fetch_or(p, v, __ATOMIC_ACQ_REL);
 }

@@ -287,7 +287,6 @@ void launch(const char* name, void (*entry)(void**), uint32_t grid, uint32_t blo
 extern "C" {
 void fs_upsweep_k32(FsArgs);
 void fs_upsweep_k64(FsArgs);
-void fs_plan(FsArgs);
 void fs_onesweep_k32(FsArgs, uint32_t);
 void fs_onesweep_k32_v(FsArgs, uint32_t);
 void fs_onesweep_k64(FsArgs, uint32_t);
@@ -309,7 +308,6 @@ struct emu_function {
 static emu_function g_funcs[] = {
     {"fs_upsweep_k32", [](void** p) { fs_upsweep_k32(A0); }},
     {"fs_upsweep_k64", [](void** p) { fs_upsweep_k64(A0); }},
-    {"fs_plan", [](void** p) { fs_plan(A0); }},
     {"fs_onesweep_k32", [](void** p) { fs_onesweep_k32(A0, D1); }},
     {"fs_onesweep_k32_v", [](void** p) { fs_onesweep_k32_v(A0, D1); }},
     {"fs_onesweep_k64", [](void** p) { fs_onesweep_k64(A0, D1); }},
