@@ -6,7 +6,7 @@
 // :1520-1639, encode_sort_pipeline_64 :1302-1478) with HIP: one device, one
 // stream, the gfx950 code object loaded by hipModuleLoad, grow-only scratch
 // in HBM, and a fixed launch sequence per sort:
-//   fs_upsweep (its last block writes the schedule) -> fs_onesweep x digits -> fs_finish
+//   fs_upsweep (its last block writes the schedule) -> fs_onesweep x digits
 // The sequence never reads anything back to the host, so fs_encode is fully
 // asynchronous; which digit passes really run is decided on the device.
 //
@@ -39,10 +39,10 @@ struct ProfEntry {
 
 const char* const kKernelNames[] = {
     "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
-    "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_finish", "fs_iota",
+    "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota",
 };
 enum {
-    K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_FINISH, K_IOTA, K_COUNT
+    K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_COUNT
 };
 
 }  // namespace
@@ -309,11 +309,6 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         void* args2[] = {&a, &digit};
         if ((r = launch(s, os, num_tiles, s->block[var], args2, st)) != FS_OK) return r;
     }
-    // fs_finish mostly finds nothing to do (every schedule but a single
-    // in-place pass ends in the caller's buffers): a small grid exits fast.
-    uint64_t fin_blocks = (n + 255) / 256;
-    if (fin_blocks > (uint64_t)s->num_cus * 2) fin_blocks = (uint64_t)s->num_cus * 2;
-    if ((r = launch(s, K_FINISH, (unsigned)fin_blocks, 256, args1, st)) != FS_OK) return r;
     s->last_stream = st;
     s->pending = true;
     return FS_OK;

@@ -114,10 +114,11 @@
 #define FS_XF_SIGN 1u      // i32/i64: xor the sign bit (self-inverse)
 #define FS_XF_FLOAT 2u     // f32/f64: FloatFlip forward, IFloatFlip inverse
 
-// Finish step after the last pass.
-#define FS_FIN_NONE 0u
-#define FS_FIN_COPY 1u     // copy keys (and values) scratch -> caller buffer
-#define FS_FIN_IOTA 2u     // argsort with every digit constant: indices = 0..n-1
+// Side duty of a digit-pass launch whose digit is constant (bits 24-31 of its
+// schedule word 2j; its word 2j+1 then names the buffers):
+#define FS_DUTY_NONE 0u
+#define FS_DUTY_COPY 1u    // copy keys (and values) between the buffers named, over the grid
+#define FS_DUTY_IOTA 2u    // argsort with every digit constant: indices = 0..n-1
 
 // Error bits reported through the host-visible status word.
 #define FS_DEVERR_LOOKBACK_TIMEOUT 1u
@@ -133,15 +134,13 @@
 #define FS_BUF_S2K 4u
 #define FS_BUF_S1V 5u
 #define FS_BUF_S2V 6u
-// per digit j: word 2j   = active | exec_index << 8 | flags << 16
+// per digit j: word 2j   = active | exec_index << 8 | flags << 16 | duty << 24
 //              word 2j+1 = src_k | dst_k << 8 | src_v << 16 | dst_v << 24 (buffer ids)
 #define FS_PLAN_PASS_WORDS 2
 #define FS_PLAN_NPASSES (FS_MAX_DIGITS * FS_PLAN_PASS_WORDS)      // passes that run
-#define FS_PLAN_FINISH (FS_PLAN_NPASSES + 1)                       // FS_FIN_*
-#define FS_PLAN_MASK (FS_PLAN_NPASSES + 2)                         // bit j: digit j sorted
-#define FS_PLAN_FINBUF (FS_PLAN_NPASSES + 3)                       // finish buffer ids, as word 2j+1
-#define FS_PLAN_TICKET (FS_PLAN_NPASSES + 4)                       // upsweep blocks finished (0 between sorts)
-#define FS_PLAN_WORDS (FS_PLAN_NPASSES + 5)
+#define FS_PLAN_MASK (FS_PLAN_NPASSES + 1)                         // bit j: digit j sorted
+#define FS_PLAN_TICKET (FS_PLAN_NPASSES + 2)                       // upsweep blocks finished (0 between sorts)
+#define FS_PLAN_WORDS (FS_PLAN_NPASSES + 3)
 
 // Error bits additionally reported through the status word.
 #define FS_DEVERR_BAD_TILE 2u        // a digit pass block mapped to a tile >= num_tiles

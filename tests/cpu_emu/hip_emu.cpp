@@ -291,7 +291,6 @@ void fs_onesweep_k32(FsArgs, uint32_t);
 void fs_onesweep_k32_v(FsArgs, uint32_t);
 void fs_onesweep_k64(FsArgs, uint32_t);
 void fs_onesweep_k64_v(FsArgs, uint32_t);
-void fs_finish(FsArgs);
 void fs_iota(uint32_t*, uint64_t);
 void fs_gather_elems(uint64_t, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint64_t);
 extern uint32_t fs_kernel_tile_keys[4];
@@ -312,7 +311,6 @@ static emu_function g_funcs[] = {
     {"fs_onesweep_k32_v", [](void** p) { fs_onesweep_k32_v(A0, D1); }},
     {"fs_onesweep_k64", [](void** p) { fs_onesweep_k64(A0, D1); }},
     {"fs_onesweep_k64_v", [](void** p) { fs_onesweep_k64_v(A0, D1); }},
-    {"fs_finish", [](void** p) { fs_finish(A0); }},
     {"fs_iota", [](void** p) { fs_iota(*(uint32_t**)p[0], *(uint64_t*)p[1]); }},
     {"fs_gather_elems", [](void** p) {
          fs_gather_elems(*(uint64_t*)p[0], *(uint64_t*)p[1], *(uint64_t*)p[2], *(uint64_t*)p[3],

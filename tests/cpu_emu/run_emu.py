@@ -41,6 +41,14 @@ def keys_for(kind, n, dist, seed):
         b = np.full(n, 7, dtype=BITS[kind])
     elif dist == "low12":
         b = g.integers(0, 1 << 12, size=n, dtype=BITS[kind])
+    elif dist == "byte0":
+        # one varying digit (the lowest): a single-pass schedule whose pass
+        # writes scratch, copied back afterwards
+        b = g.integers(0, 256, size=n, dtype=BITS[kind])
+    elif dist == "byte1":
+        # one varying digit above the lowest: the caller's keys are copied to
+        # scratch first and the single pass writes them back
+        b = (g.integers(0, 256, size=n, dtype=BITS[kind]) << BITS[kind](8)).astype(BITS[kind])
     elif dist == "zipf":
         # a dominant bin: Zipf(1.1) ranks below 2^20 (most keys small, digit 1
         # and 2 mostly zero), as in the pairs benchmark config

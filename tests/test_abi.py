@@ -36,7 +36,7 @@ def test_code_object_is_gfx950():
     # hipcc --genco writes a clang offload bundle holding the gfx950 ELF
     assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
     assert b"gfx950" in blob
-    for k in (b"fs_upsweep_k32", b"fs_upsweep_k64", b"fs_onesweep_k32", b"fs_onesweep_k64_v", b"fs_finish"):
+    for k in (b"fs_upsweep_k32", b"fs_upsweep_k64", b"fs_onesweep_k32", b"fs_onesweep_k64_v", b"fs_iota"):
         assert k in blob
 
 

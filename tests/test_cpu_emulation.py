@@ -57,6 +57,9 @@ SMALL_CASES = [
     "argsort:f64:1025:uniform:25",
     # GpuGather
     "gather:u32:5000:uniform:26", "gather:u64:3001:uniform:27",
+    # one varying digit: single-pass schedules (copy after / copy before the pass)
+    "sort:u32:5000:byte0:31", "sort:i64:3000:byte1:32", "pairs:u32:4000:byte1:33",
+    "pairs:f64:2000:byte0:34", "argsort:u32:3000:byte1:35", "sort:f32:4100:byte1:36",
     # dominant bins: histogram atomics of the shared digit added once per wave
     "sort:u32:9000:zipf:28", "pairs:u32:7000:zipf:29", "argsort:u64:3000:zipf:30",
 ]

@@ -126,6 +126,10 @@ def make_keys(kind, n, dist, seed):
         b = g.choice(g.integers(0, hi, size=7, dtype=BITS[kind], endpoint=False), size=n)
     elif dist == "lowbits":
         b = g.integers(0, 1 << 12, size=n, dtype=BITS[kind])
+    elif dist == "byte0":       # one varying digit, the lowest: single pass, then copy back
+        b = g.integers(0, 256, size=n, dtype=BITS[kind])
+    elif dist == "byte1":       # one varying digit above it: copy to scratch, then single pass
+        b = (g.integers(0, 256, size=n, dtype=BITS[kind]) << BITS[kind](8)).astype(BITS[kind])
     else:
         raise ValueError(dist)
     keys = b.view(NP[kind])
@@ -231,6 +235,24 @@ def test_deterministic(sorter):
     a = sorter.argsort_f32(keys)
     b = sorter.argsort_f32(keys)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("dist", ["byte0", "byte1"])
+@pytest.mark.parametrize("kind", KINDS)
+def test_single_pass_schedules(sorter, kind, dist):
+    """Exactly one digit varies: the in-place sort runs one pass and moves the
+    result to the caller's buffer through scratch (after the pass for the
+    lowest digit, before it otherwise); argsort writes indices directly."""
+    n = 300_007
+    keys = make_keys(kind, n, dist, seed=17)
+    check_sort(sorter, kind, keys)
+    passes, mask = sorter.last_pass_info()
+    assert passes == 1 and mask == (1 if dist == "byte0" else 2)
+    check_argsort(sorter, kind, keys)
+    if kind != "f64":                     # sort_pairs_{u32,i32,f32,u64,i64} (lib.rs)
+        vals = np.random.Generator(np.random.PCG64(5)).integers(0, 1 << 32, size=n, dtype=np.uint32)
+        check_pairs(sorter, kind, keys, vals)
+    check_buffer(sorter, kind, keys)
 
 
 def test_constant_digit_passes_skipped(sorter):
