@@ -353,6 +353,35 @@ def test_more_than_2_30_keys(sorter):
     assert int((k64 * k64).sum()) == int((o64 * o64).sum())
 
 
+def test_n_within_a_tile_of_2_32(sorter):
+    """n = 2^32 - 1, the largest length: the last tile's key indices run past
+    2^32 (they are kept in 64 bits).  Keys i & 0xFFFF, so two digits vary;
+    value v then occurs (n - 1 - v) // 65536 + 1 times, and the output is
+    checked against that closed form: ascending, and every value's first and
+    last positions where the counts put them."""
+    n = (1 << 32) - 1
+    keys = np.arange(n, dtype=np.uint32)
+    keys &= np.uint32(0xFFFF)
+    buf = sorter.alloc_sort_buffer("u32", n)
+    buf.copy_from_slice(keys)
+    del keys
+    sorter.sort_buffer(buf)
+    passes, mask = sorter.last_pass_info()
+    assert passes == 2 and mask == 0b11
+    out = buf.as_slice()
+    buf.free()
+    step = 1 << 28
+    for s0 in range(0, n, step):
+        c = out[s0:min(n, s0 + step + 1)]
+        assert bool(np.all(c[1:] >= c[:-1])), f"not ascending near {s0}"
+    v = np.arange(1 << 16, dtype=np.int64)
+    counts = (n - 1 - v) // (1 << 16) + 1
+    first = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    assert int(counts.sum()) == n
+    assert np.array_equal(np.searchsorted(out, v.astype(np.uint32), side="left"), first)
+    assert np.array_equal(out[first + counts - 1].astype(np.int64), v)
+
+
 @pytest.mark.parametrize("kind", ["u32", "f32", "u64", "i64"])
 def test_device_keys_off_16_byte_boundary(sorter, kind):
     """Keys one element past a 16-byte boundary (e.g. a slice of a larger
