@@ -554,6 +554,54 @@ def hip_stream():
     hip.hipStreamDestroy(st)
 
 
+def test_graph_capture_replays(hip_stream):
+    """The sort is capturable into a HIP graph: fs_encode on a capturing stream
+    records kernel launches only (no memset; the scratch has grown beforehand,
+    and the kernels reset the histogram, the upsweep ticket and the look-back
+    entries themselves).  Each replay sorts new data with its own device-side
+    schedule (4, 4, 2 and 1 passes), eager sorts run between the replays, and
+    every replay matches the oracle."""
+    import ctypes
+    from forge_sort import OP_PAIRS, GpuSorter
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    st = ctypes.c_void_p(hip_stream)
+    s = GpuSorter.with_context(0, hip_stream)
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    try:
+        n = 1_000_003
+        g = np.random.Generator(np.random.PCG64(904))
+        kb, vb = s.alloc_sort_buffer("u32", n), s.alloc_sort_buffer("u32", n)
+        kb.copy_from_slice(make_keys("u32", n, "uniform", seed=900))
+        vb.copy_from_slice(g.integers(0, 1 << 32, size=n, dtype=np.uint32))
+        s.encode(OP_PAIRS, "u32", kb.device_ptr(), vb.device_ptr(), n, stream=hip_stream)
+        s.synchronize()                       # scratch grown: the captured sort allocates nothing
+        assert hip.hipStreamBeginCapture(st, 0) == 0
+        s.encode(OP_PAIRS, "u32", kb.device_ptr(), vb.device_ptr(), n, stream=hip_stream)
+        assert hip.hipStreamEndCapture(st, ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
+        for r, dist in enumerate(["uniform", "few", "lowbits", "byte1"]):
+            keys = make_keys("u32", n, dist, seed=910 + r)
+            vals = g.integers(0, 1 << 32, size=n, dtype=np.uint32)
+            kb.copy_from_slice(keys)
+            vb.copy_from_slice(vals)
+            assert hip.hipGraphLaunch(exe, st) == 0
+            assert hip.hipStreamSynchronize(st) == 0
+            ek, ev = oracle.sort_pairs("u32", keys, vals)
+            assert np.array_equal(kb.as_slice(), ek) and np.array_equal(vb.as_slice(), ev), f"replay {r} ({dist})"
+            other = make_keys("u32", 200_001, "uniform", seed=950 + r)   # eager work between replays
+            got = other.copy()
+            s.sort_u32(got)
+            assert np.array_equal(got, oracle.sort("u32", other))
+        kb.free()
+        vb.free()
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        s.close()
+
+
 def test_with_context_caller_stream(hip_stream):
     """GpuSorter::with_context on the caller's stream (lib.rs:606-686): every op
     and the async encode run there; results match the oracle."""
