@@ -17,7 +17,7 @@
 #define FS_K32_BLOCK 768
 #endif
 #ifndef FS_K32_ITEMS
-#define FS_K32_ITEMS 16
+#define FS_K32_ITEMS 21
 #endif
 #ifndef FS_K32V_BLOCK
 #define FS_K32V_BLOCK 768
@@ -29,13 +29,18 @@
 #define FS_K64_BLOCK 768
 #endif
 #ifndef FS_K64_ITEMS
-#define FS_K64_ITEMS 8
+#define FS_K64_ITEMS 10
 #endif
 #ifndef FS_K64V_BLOCK
 #define FS_K64V_BLOCK 768
 #endif
 #ifndef FS_K64V_ITEMS
-#define FS_K64V_ITEMS 8
+#define FS_K64V_ITEMS 10
+#endif
+// Items whose LDS reads the staging and store loops keep in flight at once
+// (0: all of a thread's items).
+#ifndef FS_STAGE_BATCH
+#define FS_STAGE_BATCH 0
 #endif
 // index into fs_kernel_tile_keys
 #define FS_VAR_K32 0
