@@ -23,7 +23,7 @@
 #define FS_K32V_BLOCK 768
 #endif
 #ifndef FS_K32V_ITEMS
-#define FS_K32V_ITEMS 12
+#define FS_K32V_ITEMS 18
 #endif
 #ifndef FS_K64_BLOCK
 #define FS_K64_BLOCK 768

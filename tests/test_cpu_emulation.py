@@ -70,7 +70,7 @@ PROD_CASES = [
     "sort:f64:9000:uniform:8", "argsort:i32:13000:uniform:9",
     "pairs:u32:30000:zipf:10", "sort:u32:26000:few:11",
     # one key past a tile of the u32 (768 x 21) and u64 (768 x 10) variants
-    "sort:u32:16129:uniform:12", "sort:u64:7681:uniform:13",
+    "sort:u32:16129:uniform:12", "sort:u64:7681:uniform:13", "pairs:u32:13825:uniform:14",
 ]
 
 
