@@ -17,7 +17,7 @@
 #define FS_K32_BLOCK 768
 #endif
 #ifndef FS_K32_ITEMS
-#define FS_K32_ITEMS 21
+#define FS_K32_ITEMS 23
 #endif
 #ifndef FS_K32V_BLOCK
 #define FS_K32V_BLOCK 768

@@ -69,8 +69,8 @@ PROD_CASES = [
     "pairs:u64:20000:uniform:4", "sort:i64:20000:low12:6", "pairs:u32:25000:few:7",
     "sort:f64:9000:uniform:8", "argsort:i32:13000:uniform:9",
     "pairs:u32:30000:zipf:10", "sort:u32:26000:few:11",
-    # one key past a tile of the u32 (768 x 21) and u64 (768 x 10) variants
-    "sort:u32:16129:uniform:12", "sort:u64:7681:uniform:13", "pairs:u32:13825:uniform:14",
+    # one key past a tile of the u32 (768 x 23), u64 (768 x 10) and u32+values (768 x 18) variants
+    "sort:u32:17665:uniform:12", "sort:u64:7681:uniform:13", "pairs:u32:13825:uniform:14",
 ]
 
 
