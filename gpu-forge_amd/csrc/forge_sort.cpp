@@ -281,12 +281,12 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.tile = tile;
     a.vec_ok = ((uintptr_t)keys % 16 == 0) ? 1u : 0u;
     // upsweep: blocks over contiguous runs of tiles, per CU 32 for 32-bit keys
-    // and 16 for 64-bit keys (measured best on MI355X: 256M u32 0.325 ->
-    // 0.313 ms at 32; 128M u64 0.366 ms at 16, 0.379 at 32);
-    // FS_UPSWEEP_BLOCKS_PER_CU overrides both
+    // and 12 for 64-bit keys (measured best on MI355X with the current tiles:
+    // 256M u32 0.316 ms at 24-48, 0.375 at 64; 128M u64 0.360 ms at 12, 0.382
+    // at 16, 0.368 at 32); FS_UPSWEEP_BLOCKS_PER_CU overrides both
     static const uint32_t up_env = getenv("FS_UPSWEEP_BLOCKS_PER_CU")
                                        ? (uint32_t)atoi(getenv("FS_UPSWEEP_BLOCKS_PER_CU")) : 0u;
-    const uint32_t up_per_cu = up_env ? up_env : (key64(t) ? 16u : 32u);
+    const uint32_t up_per_cu = up_env ? up_env : (key64(t) ? 12u : 32u);
     const uint32_t up_blocks_target = (uint32_t)s->num_cus * up_per_cu;
     const uint32_t tpb = (num_tiles + up_blocks_target - 1) / up_blocks_target;
     a.hist_tiles_per_block = tpb;
