@@ -280,16 +280,17 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.wide = wide ? 1u : 0u;
     a.tile = tile;
     a.vec_ok = ((uintptr_t)keys % 16 == 0) ? 1u : 0u;
-    // upsweep: blocks over contiguous runs of tiles, per CU 32 for 32-bit keys
-    // and 12 for 64-bit keys (measured best on MI355X with the current tiles:
-    // 256M u32 0.316 ms at 24-48, 0.375 at 64; 128M u64 0.360 ms at 12, 0.382
-    // at 16, 0.368 at 32); FS_UPSWEEP_BLOCKS_PER_CU overrides both
+    // upsweep: 2 blocks per CU (the blocks' 64 KiB of counters allow two
+    // resident), fewer when the keys give each block less than one step of
+    // FS_UPSWEEP_UNROLL units per thread; FS_UPSWEEP_BLOCKS_PER_CU overrides
     static const uint32_t up_env = getenv("FS_UPSWEEP_BLOCKS_PER_CU")
                                        ? (uint32_t)atoi(getenv("FS_UPSWEEP_BLOCKS_PER_CU")) : 0u;
-    const uint32_t up_per_cu = up_env ? up_env : (key64(t) ? 12u : 32u);
-    const uint32_t up_blocks_target = (uint32_t)s->num_cus * up_per_cu;
-    const uint32_t tpb = (num_tiles + up_blocks_target - 1) / up_blocks_target;
-    a.hist_tiles_per_block = tpb;
+    const uint64_t up_per_cu = up_env ? up_env : 2u;
+    const uint64_t up_units = a.vec_ok ? n / (16u / key_bytes(t)) : n;
+    const uint64_t up_span = (uint64_t)FS_UPSWEEP_UNROLL * FS_HIST_BLOCK;
+    uint64_t up_blocks = (up_units + up_span - 1) / up_span;
+    if (up_blocks > (uint64_t)s->num_cus * up_per_cu) up_blocks = (uint64_t)s->num_cus * up_per_cu;
+    if (up_blocks == 0) up_blocks = 1;
     a.keys = (uint64_t)(uintptr_t)keys;
     a.vals = (uint64_t)(uintptr_t)vals;
     a.s1k = (uint64_t)(uintptr_t)s->s1k.p;
@@ -304,7 +305,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 
-    const unsigned up_grid = (num_tiles + tpb - 1) / tpb;
+    const unsigned up_grid = (unsigned)up_blocks;
     void* args1[] = {&a};
     if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st)) != FS_OK) return r;
     const int os = K_OS32 + var;   // kernel order matches FS_VAR_*

@@ -55,9 +55,24 @@
 #endif
 
 // Upsweep (all-digit histogram) block, and 16-byte loads in flight per lane.
-#define FS_HIST_BLOCK 256
+#ifndef FS_HIST_BLOCK
+#define FS_HIST_BLOCK 1024
+#endif
 #ifndef FS_UPSWEEP_UNROLL
 #define FS_UPSWEEP_UNROLL 4
+#endif
+// Upsweep counter replicas (lanes with equal lane % replicas share a counter:
+// 32 keeps every lane of a half-wave on its own LDS bank) and the vectors per
+// lane between two folds of the 16-bit counters into the histogram.  64 KiB
+// of LDS for both key widths.
+#ifndef FS_UP_REPLICAS_K32
+#define FS_UP_REPLICAS_K32 32
+#endif
+#ifndef FS_UP_REPLICAS_K64
+#define FS_UP_REPLICAS_K64 16
+#endif
+#ifndef FS_UP_CHUNK_STEPS
+#define FS_UP_CHUNK_STEPS 256
 #endif
 
 // Look-back tile entries, one per (tile, digit), in a single chain over all
@@ -161,7 +176,6 @@ typedef struct FsArgs {
     uint32_t digits;            // 4 or 8
     uint32_t num_tiles;         // ceil(n / tile)
     uint32_t wide;              // 1: 64-bit look-back tile entries (n >= FS_LB_WIDE_KEYS)
-    uint32_t hist_tiles_per_block;  // tiles per upsweep block
     uint32_t tile;              // keys per tile of the digit-pass variant in use
     uint32_t vec_ok;            // keys pointer is 16-byte aligned
     uint32_t pad2;

@@ -62,6 +62,8 @@ SMALL_CASES = [
     "pairs:f64:2000:byte0:34", "argsort:u32:3000:byte1:35", "sort:f32:4100:byte1:36",
     # dominant bins: histogram atomics of the shared digit added once per wave
     "sort:u32:9000:zipf:28", "pairs:u32:7000:zipf:29", "argsort:u64:3000:zipf:30",
+    # several upsweep steps and counter folds per block
+    "sort:u64:9000:uniform:37", "sort:u32:9000:same:38", "sort:i64:9000:zipf:39",
 ]
 
 PROD_CASES = [
