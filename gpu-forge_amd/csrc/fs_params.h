@@ -94,7 +94,7 @@
 #define FS_XCDS 8
 #endif
 #ifndef FS_XCD_TILES
-#define FS_XCD_TILES 4
+#define FS_XCD_TILES 8
 #endif
 
 // Predecessor tile entries read per look-back round trip.

@@ -118,7 +118,8 @@ def test_emulated_upsweep_long_segments(emulator):
 
 def test_emulated_single_dispatch_queue(emulator):
     """Blocks started in plain increasing order from one queue (not dealt over
-    XCDs), 40 at a time: a digit-pass tile then may wait on a tile whose block
-    starts up to 31 blocks later, which the resident blocks allow."""
+    XCDs), 72 at a time: a digit-pass tile then may wait on a tile whose block
+    starts up to 63 blocks later (8 XCDs x 8 tiles per round), which the
+    resident blocks allow."""
     run_cases("small", ["sort:u32:70000:uniform:2", "pairs:u32:40000:uniform:7", "sort:u64:9000:uniform:3"],
-              env={"EMU_XCDS": "1", "EMU_WORKERS": "40"})
+              env={"EMU_XCDS": "1", "EMU_WORKERS": "72"})
