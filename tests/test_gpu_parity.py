@@ -334,6 +334,31 @@ def test_wide_lookback_entries(sorter, force_wide_lookback, kind):
                 np.arange(100_000, dtype=np.uint32)[::-1].copy())
 
 
+def test_upsweep_counter_folds_u64(sorter):
+    """300M equal u64 keys: each upsweep block counts several chunks, and every
+    16-bit counter of the one occupied bin takes its largest per-chunk count
+    before each fold.  The histogram must still be exact: all 8 digits are
+    found constant, no pass runs, and the keys are unchanged.  Then one key
+    differs in its low byte: digit 0 alone must be found varying (one pass)."""
+    n = 300_000_000
+    c = np.uint64(0x0123456789ABCDEF)
+    keys = np.full(n, c, dtype=np.uint64)
+    buf = sorter.alloc_sort_buffer("u64", n)
+    buf.copy_from_slice(keys)
+    sorter.sort_u64_buffer(buf)
+    assert sorter.last_pass_info() == (0, 0)
+    out = buf.as_slice()
+    assert bool(np.all(out == c))
+    keys[n // 2] = c ^ np.uint64(0x5A)           # one key differs in its low byte
+    buf.copy_from_slice(keys)
+    sorter.sort_u64_buffer(buf)
+    assert sorter.last_pass_info() == (1, 0b1)
+    out = buf.as_slice()
+    buf.free()
+    # c's low byte is 0xEF; the odd key's is 0xB5, so it sorts first
+    assert int(out[0]) == int(c ^ np.uint64(0x5A)) and bool(np.all(out[1:] == c))
+
+
 def test_more_than_2_30_keys(sorter):
     """n = 2^30 + 12345 u32 keys: inclusive prefixes exceed 30 bits, so the
     64-bit look-back entries are in use.  Checked without the oracle (too slow
