@@ -72,6 +72,14 @@ struct fs_sorter {
     std::vector<ProfEntry> prof;         // launches since profiling was enabled or reset
     std::vector<hipEvent_t> event_pool;
 
+    // Slice API staging: two pinned host chunks, copied by the CPU while the
+    // DMA engine moves the other (allocated on the first slice call).
+    // pin_busy[b]: a copy that reads or writes pin[b] was enqueued and
+    // pin_ev[b] (recorded after it) has not been waited on since.
+    void* pin[2] = {nullptr, nullptr};
+    hipEvent_t pin_ev[2] = {nullptr, nullptr};
+    bool pin_busy[2] = {false, false};
+
     std::string err;
 };
 
@@ -457,6 +465,10 @@ void fs_sorter_free(fs_sorter* s) {
     if (s->plan) (void)hipFree(s->plan);
     if (s->stats) (void)hipFree(s->stats);
     if (s->status) (void)hipHostFree(s->status);
+    for (int b = 0; b < 2; ++b) {
+        if (s->pin[b]) (void)hipHostFree(s->pin[b]);
+        if (s->pin_ev[b]) (void)hipEventDestroy(s->pin_ev[b]);
+    }
     if (s->module) (void)hipModuleUnload(s->module);
     if (s->own_stream && s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
@@ -563,6 +575,60 @@ fs_status fs_sort_pairs_buffer(fs_sorter* s, fs_key_type type, void* device_keys
     return sync_and_check(s);
 }
 
+// Slice API staging: chunks of FS_PIN_CHUNK bytes through two pinned host
+// buffers, so that the CPU copy of one chunk overlaps the DMA of the other (a
+// pageable hipMemcpy stages through the runtime's own buffers one piece at a
+// time).
+#ifndef FS_PIN_CHUNK
+#define FS_PIN_CHUNK (8u << 20)
+#endif
+static fs_status ensure_pinned(fs_sorter* s) {
+    for (int b = 0; b < 2; ++b) {
+        if (!s->pin[b]) HIP_TRY(s, hipHostMalloc(&s->pin[b], FS_PIN_CHUNK, hipHostMallocDefault));
+        if (!s->pin_ev[b]) HIP_TRY(s, hipEventCreate(&s->pin_ev[b]));
+    }
+    return FS_OK;
+}
+static fs_status stage_to_device(fs_sorter* s, void* dev, const void* host, size_t bytes) {
+    for (size_t off = 0, i = 0; off < bytes; off += FS_PIN_CHUNK, ++i) {
+        const size_t len = bytes - off < FS_PIN_CHUNK ? bytes - off : FS_PIN_CHUNK;
+        const int b = (int)(i & 1);
+        // The last DMA out of pin[b] (this call's or an earlier staging call's)
+        // must be done before the CPU overwrites it.
+        if (s->pin_busy[b]) HIP_TRY(s, hipEventSynchronize(s->pin_ev[b]));
+        s->pin_busy[b] = false;
+        memcpy(s->pin[b], (const char*)host + off, len);
+        HIP_TRY(s, hipMemcpyAsync((char*)dev + off, s->pin[b], len, hipMemcpyHostToDevice, s->stream));
+        HIP_TRY(s, hipEventRecord(s->pin_ev[b], s->stream));
+        s->pin_busy[b] = true;
+    }
+    return FS_OK;
+}
+static fs_status stage_to_host(fs_sorter* s, void* host, const void* dev, size_t bytes) {
+    const size_t chunks = (bytes + FS_PIN_CHUNK - 1) / FS_PIN_CHUNK;
+    auto issue = [&](size_t i) -> fs_status {
+        const size_t off = i * FS_PIN_CHUNK;
+        const size_t len = bytes - off < FS_PIN_CHUNK ? bytes - off : FS_PIN_CHUNK;
+        // stream order puts this DMA after any earlier one that reads pin[i & 1]
+        HIP_TRY(s, hipMemcpyAsync(s->pin[i & 1], (const char*)dev + off, len, hipMemcpyDeviceToHost, s->stream));
+        HIP_TRY(s, hipEventRecord(s->pin_ev[i & 1], s->stream));
+        s->pin_busy[i & 1] = true;
+        return FS_OK;
+    };
+    fs_status r;
+    for (size_t i = 0; i < chunks && i < 2; ++i)
+        if ((r = issue(i)) != FS_OK) return r;
+    for (size_t i = 0; i < chunks; ++i) {
+        const size_t off = i * FS_PIN_CHUNK;
+        const size_t len = bytes - off < FS_PIN_CHUNK ? bytes - off : FS_PIN_CHUNK;
+        HIP_TRY(s, hipEventSynchronize(s->pin_ev[i & 1]));
+        s->pin_busy[i & 1] = false;
+        memcpy((char*)host + off, s->pin[i & 1], len);
+        if (i + 2 < chunks && (r = issue(i + 2)) != FS_OK) return r;
+    }
+    return FS_OK;
+}
+
 // Slice API: stage through the sorter's own device buffers, like the
 // reference's memcpy into buf_a (lib.rs:800-806) and back (:828-834).
 static fs_status host_op(fs_sorter* s, fs_op op, fs_key_type type, void* keys, uint32_t* vals, uint64_t n) {
@@ -582,14 +648,12 @@ static fs_status host_op(fs_sorter* s, fs_op op, fs_key_type type, void* keys, u
     const size_t kb = key_bytes(type);
     if ((r = ensure(s, s->iok, n * kb)) != FS_OK) return r;
     if (op != FS_OP_SORT && (r = ensure(s, s->iov, n * 4)) != FS_OK) return r;
-    HIP_TRY(s, hipMemcpyAsync(s->iok.p, keys, n * kb, hipMemcpyHostToDevice, s->stream));
-    if (op == FS_OP_PAIRS)
-        HIP_TRY(s, hipMemcpyAsync(s->iov.p, vals, n * 4, hipMemcpyHostToDevice, s->stream));
+    if ((r = ensure_pinned(s)) != FS_OK) return r;
+    if ((r = stage_to_device(s, s->iok.p, keys, n * kb)) != FS_OK) return r;
+    if (op == FS_OP_PAIRS && (r = stage_to_device(s, s->iov.p, vals, n * 4)) != FS_OK) return r;
     if ((r = enqueue(s, op, type, s->iok.p, (uint32_t*)s->iov.p, n, s->stream)) != FS_OK) return r;
-    if (op != FS_OP_ARGSORT)
-        HIP_TRY(s, hipMemcpyAsync(keys, s->iok.p, n * kb, hipMemcpyDeviceToHost, s->stream));
-    if (op != FS_OP_SORT)
-        HIP_TRY(s, hipMemcpyAsync(vals, s->iov.p, n * 4, hipMemcpyDeviceToHost, s->stream));
+    if (op != FS_OP_ARGSORT && (r = stage_to_host(s, keys, s->iok.p, n * kb)) != FS_OK) return r;
+    if (op != FS_OP_SORT && (r = stage_to_host(s, vals, s->iov.p, n * 4)) != FS_OK) return r;
     return sync_and_check(s);
 }
 

@@ -193,4 +193,5 @@ hipError_t hipModuleLaunchKernel(hipFunction_t, unsigned, unsigned, unsigned, un
 hipError_t hipEventCreate(hipEvent_t*);
 hipError_t hipEventDestroy(hipEvent_t);
 hipError_t hipEventRecord(hipEvent_t, hipStream_t);
+hipError_t hipEventSynchronize(hipEvent_t);
 hipError_t hipEventElapsedTime(float*, hipEvent_t, hipEvent_t);

@@ -368,8 +368,10 @@ hipError_t hipMalloc(void** p, size_t n) {
     return hipSuccess;
 }
 
+namespace { void flush_copies(); }
 hipError_t hipFree(void* p) {
     if (!p) return hipSuccess;
+    flush_copies();
     std::lock_guard<std::mutex> g(g_mu);
     auto it = g_allocs.find(p);
     if (it == g_allocs.end()) return hipErrorInvalidValue;
@@ -378,12 +380,31 @@ hipError_t hipFree(void* p) {
     return hipSuccess;
 }
 
+// Asynchronous copies are deferred, as a DMA engine may run them late: they
+// take place, in issue order, at the next point that waits for the stream or
+// runs stream-ordered work (a launch, a synchronous copy or memset, an event
+// or stream wait, a free).  Host code that reuses a source buffer, or reads a
+// destination, before waiting then sees what real hardware may show it.
+namespace {
+struct emu_copy { void* d; const void* s; size_t n; };
+std::mutex g_copy_mu;
+std::vector<emu_copy> g_pending;
+void flush_copies() {
+    std::lock_guard<std::mutex> lk(g_copy_mu);
+    for (const emu_copy& c : g_pending) memmove(c.d, c.s, c.n);
+    g_pending.clear();
+}
+}  // namespace
 hipError_t hipHostMalloc(void** p, size_t n, unsigned) { return hipMalloc(p, n); }
-hipError_t hipHostFree(void* p) { return hipFree(p); }
-hipError_t hipMemset(void* p, int v, size_t n) { memset(p, v, n); return hipSuccess; }
-hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind) { memmove(d, s, n); return hipSuccess; }
-hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t) { return hipMemcpy(d, s, n, k); }
-hipError_t hipMemcpyDtoH(void* d, hipDeviceptr_t s, size_t n) { memcpy(d, s, n); return hipSuccess; }
+hipError_t hipHostFree(void* p) { flush_copies(); return hipFree(p); }
+hipError_t hipMemset(void* p, int v, size_t n) { flush_copies(); memset(p, v, n); return hipSuccess; }
+hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind) { flush_copies(); memmove(d, s, n); return hipSuccess; }
+hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind, hipStream_t) {
+    std::lock_guard<std::mutex> lk(g_copy_mu);
+    g_pending.push_back({d, s, n});
+    return hipSuccess;
+}
+hipError_t hipMemcpyDtoH(void* d, hipDeviceptr_t s, size_t n) { flush_copies(); memcpy(d, s, n); return hipSuccess; }
 
 hipError_t hipGetDeviceCount(int* c) { *c = 1; return hipSuccess; }
 hipError_t hipSetDevice(int d) { return d == 0 ? hipSuccess : hipErrorInvalidValue; }
@@ -396,8 +417,8 @@ hipError_t hipGetLastError(void) { return hipSuccess; }
 const char* hipGetErrorString(hipError_t e) { return e == hipSuccess ? "success" : "emulated HIP error"; }
 hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned) { *s = new emu_stream(); return hipSuccess; }
 hipError_t hipStreamDestroy(hipStream_t s) { delete s; return hipSuccess; }
-hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
-hipError_t hipDeviceSynchronize(void) { return hipSuccess; }
+hipError_t hipStreamSynchronize(hipStream_t) { flush_copies(); return hipSuccess; }
+hipError_t hipDeviceSynchronize(void) { flush_copies(); return hipSuccess; }
 
 hipError_t hipModuleLoad(hipModule_t* m, const char*) { *m = new emu_module(); return hipSuccess; }
 hipError_t hipModuleUnload(hipModule_t m) { delete m; return hipSuccess; }
@@ -413,12 +434,15 @@ hipError_t hipModuleGetGlobal(hipDeviceptr_t* p, size_t* sz, hipModule_t, const 
 }
 hipError_t hipModuleLaunchKernel(hipFunction_t f, unsigned gx, unsigned, unsigned, unsigned bx, unsigned,
                                  unsigned, unsigned, hipStream_t, void** params, void**) {
+    flush_copies();
     emu::launch(f->name, f->entry, gx, bx, params);
     return hipSuccess;
 }
 hipError_t hipEventCreate(hipEvent_t* e) { *e = new emu_event(); return hipSuccess; }
 hipError_t hipEventDestroy(hipEvent_t e) { delete e; return hipSuccess; }
 hipError_t hipEventRecord(hipEvent_t e, hipStream_t) { e->t = std::chrono::steady_clock::now(); return hipSuccess; }
+// launches complete before their call returns; deferred copies run here
+hipError_t hipEventSynchronize(hipEvent_t) { flush_copies(); return hipSuccess; }
 hipError_t hipEventElapsedTime(float* ms, hipEvent_t a, hipEvent_t b) {
     *ms = std::chrono::duration<float, std::milli>(b->t - a->t).count();
     return hipSuccess;
