@@ -100,6 +100,9 @@ fs_status fs_copy_to_host(fs_sorter *s, void *host_dst, const void *device_src, 
 fs_status fs_copy_device(fs_sorter *s, void *device_dst, const void *device_src, size_t bytes);
 
 /* ---- slice API: host arrays (copies in and out, like lib.rs:791-838) ------- */
+/* The copies stage through two 8 MiB pinned host buffers that the sorter
+ * allocates on its first slice call and frees in fs_sorter_free; the caller's
+ * arrays need not be pinned or aligned. */
 
 /* sort_u32 :791, sort_i32 :840, sort_f32 :920, sort_u64 :2238, sort_i64 :2348, sort_f64 :2417 */
 fs_status fs_sort(fs_sorter *s, fs_key_type type, void *host_keys, uint64_t n);
