@@ -272,6 +272,22 @@ def test_encode_sort_async(sorter):
     buf.free()
 
 
+def test_slice_staging_ragged_chunks(sorter):
+    """Slice calls stage through two 8 MiB pinned host buffers: keys and values
+    that span several chunks with a partial last one, one call after another
+    (each reuses the buffers while the previous call's copies may be the last
+    to have used them), the second call smaller than the first."""
+    chunk_u64 = (8 << 20) // 8
+    n = 3 * chunk_u64 + 12_345             # keys: 4 chunks; values: 2 chunks
+    g = np.random.Generator(np.random.PCG64(131))
+    check_pairs(sorter, "u64", datagen.uniform_u64(n, seed=132), g.integers(0, 2**32, n, dtype=np.uint32))
+    check_pairs(sorter, "f32", datagen.f32_normal_specials(n - 77_777, seed=133),
+                g.integers(0, 2**32, n - 77_777, dtype=np.uint32))
+    check_argsort(sorter, "i64", datagen.uniform_i64(2 * chunk_u64 + 1, seed=134))
+    check_sort(sorter, "f64", datagen.normal_f64(chunk_u64 + 3, seed=135))
+    check_sort(sorter, "u32", datagen.uniform_u32(5, seed=136))
+
+
 # ---- BASELINE.json configurations at full size ------------------------------------
 
 def test_config0_sort_u32_1m(sorter):
