@@ -39,10 +39,10 @@ struct ProfEntry {
 
 const char* const kKernelNames[] = {
     "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
-    "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota",
+    "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
 };
 enum {
-    K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_COUNT
+    K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_COUNT
 };
 
 }  // namespace
@@ -322,7 +322,10 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     for (uint32_t d = 0; d < a.digits; ++d) {
         uint32_t digit = d;
         void* args2[] = {&a, &digit};
-        if ((r = launch(s, os, num_tiles, s->block[var], args2, st)) != FS_OK) return r;
+        // digit 0 of a keys-only sort: its pass, when it runs, is the first,
+        // which needs no stability (same tiles as the stable kernel)
+        const int k = (d == 0 && op == FS_OP_SORT) ? (key64(t) ? K_ANY64 : K_ANY32) : os;
+        if ((r = launch(s, k, num_tiles, s->block[var], args2, st)) != FS_OK) return r;
     }
     s->last_stream = st;
     s->pending = true;

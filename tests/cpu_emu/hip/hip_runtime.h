@@ -35,6 +35,7 @@ uint64_t ballot(int pred);
 int all(int pred);
 uint32_t shfl_up(uint32_t v, unsigned off);
 uint32_t readfirstlane(uint32_t v);
+uint32_t readlane(uint32_t v, uint32_t src);
 void sleep_hint();
 void wave_barrier();
 unsigned lane();
@@ -118,6 +119,7 @@ inline uint32_t emu_mbcnt_hi(uint32_t mask, uint32_t acc) {
     return acc + (uint32_t)__builtin_popcount(mask & below);
 }
 #define __builtin_amdgcn_readfirstlane(v) emu_readfirstlane((uint32_t)(v))
+#define __builtin_amdgcn_readlane(v, l) ::emu::readlane((uint32_t)(v), (uint32_t)(l))
 #define __builtin_amdgcn_uicmp(a, b, p) emu_uicmp((uint32_t)(a), (uint32_t)(b), (p))
 #define __builtin_amdgcn_sbfe(x, o, w) emu_sbfe((int32_t)(x), (o), (w))
 #define __builtin_amdgcn_ubfe(x, o, w) emu_ubfe((uint32_t)(x), (o), (w))

@@ -41,7 +41,7 @@
 namespace emu {
 
 enum State { RUNNABLE, AT_BARRIER, AT_WAVEOP, DONE };
-enum WaveKind { WK_BALLOT, WK_ALL, WK_SHFL_UP, WK_FIRSTLANE, WK_BARRIER };
+enum WaveKind { WK_BALLOT, WK_ALL, WK_SHFL_UP, WK_FIRSTLANE, WK_BARRIER, WK_READLANE };
 
 struct Fiber {
     ucontext_t ctx;
@@ -121,6 +121,7 @@ uint64_t ballot(int p) { return wave_op(WK_BALLOT, p != 0, 0); }
 int all(int p) { return (int)wave_op(WK_ALL, p != 0, 0); }
 uint32_t shfl_up(uint32_t v, unsigned off) { return (uint32_t)wave_op(WK_SHFL_UP, v, off); }
 uint32_t readfirstlane(uint32_t v) { return (uint32_t)wave_op(WK_FIRSTLANE, v, 0); }
+uint32_t readlane(uint32_t v, uint32_t src) { return (uint32_t)wave_op(WK_READLANE, v, src); }
 // Lockstep point: lanes of a wave run one after another between wave
 // operations here, while on the GPU they execute each instruction together;
 // the kernels mark the places where that matters with a wave barrier.
@@ -174,6 +175,13 @@ static bool resolve_wave(int w) {
             case WK_ALL: f.wres = allp; break;
             case WK_FIRSTLANE: f.wres = b.f[first].wval; break;
             case WK_BARRIER: f.wres = 0; break;
+            case WK_READLANE: {
+                // the source lane must take part (the kernels only read lanes they know are active)
+                const int src = lo + (int)(f.warg & 63u);
+                if (src >= hi || b.f[src].state != AT_WAVEOP) die("readlane of a lane outside the operation");
+                f.wres = b.f[src].wval;
+                break;
+            }
             case WK_SHFL_UP: {
                 const int src = (i - lo) - (int)f.warg;
                 f.wres = (src >= 0 && b.f[lo + src].state == AT_WAVEOP) ? b.f[lo + src].wval : f.wval;
@@ -291,6 +299,8 @@ void fs_onesweep_k32(FsArgs, uint32_t);
 void fs_onesweep_k32_v(FsArgs, uint32_t);
 void fs_onesweep_k64(FsArgs, uint32_t);
 void fs_onesweep_k64_v(FsArgs, uint32_t);
+void fs_onesweep_any_k32(FsArgs, uint32_t);
+void fs_onesweep_any_k64(FsArgs, uint32_t);
 void fs_iota(uint32_t*, uint64_t);
 void fs_gather_elems(uint64_t, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint64_t);
 extern uint32_t fs_kernel_tile_keys[4];
@@ -311,6 +321,8 @@ static emu_function g_funcs[] = {
     {"fs_onesweep_k32_v", [](void** p) { fs_onesweep_k32_v(A0, D1); }},
     {"fs_onesweep_k64", [](void** p) { fs_onesweep_k64(A0, D1); }},
     {"fs_onesweep_k64_v", [](void** p) { fs_onesweep_k64_v(A0, D1); }},
+    {"fs_onesweep_any_k32", [](void** p) { fs_onesweep_any_k32(A0, D1); }},
+    {"fs_onesweep_any_k64", [](void** p) { fs_onesweep_any_k64(A0, D1); }},
     {"fs_iota", [](void** p) { fs_iota(*(uint32_t**)p[0], *(uint64_t*)p[1]); }},
     {"fs_gather_elems", [](void** p) {
          fs_gather_elems(*(uint64_t*)p[0], *(uint64_t*)p[1], *(uint64_t*)p[2], *(uint64_t*)p[3],
