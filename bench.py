@@ -110,57 +110,57 @@ def ordered_bits(a):
 
 
 def check_output(op, keys_in, vals_in, keys_out, vals_out):
-    """Sorted in the key order, same multiset; argsort/pairs: stable (ties by
-    original index, values being the original index for the pairs input)."""
-    ok = True
+    """Bit-for-bit equality with the one correct output, computed by numpy on
+    the keys' total-order bits: sorted keys (unique for a multiset), and for
+    argsort and pairs the stable order (ties by original index)."""
+    o = ordered_bits(keys_in)
+    if op == "sort":
+        return bool(np.array_equal(ordered_bits(keys_out), np.sort(o)))
+    idx = np.argsort(o, kind="stable").astype(np.uint32)
     if op == "argsort":
-        idx = vals_out.astype(np.int64)
-        ok &= bool(np.array_equal(np.sort(idx), np.arange(idx.size)))
-        o = ordered_bits(keys_in[idx])
-    else:
-        o = ordered_bits(keys_out)
-        u_in = keys_in.view(o.dtype)
-        u_out = keys_out.view(o.dtype)
-        ok &= int(u_in.astype(np.uint64).sum()) == int(u_out.astype(np.uint64).sum())
-        ok &= int(np.bitwise_xor.reduce(u_in)) == int(np.bitwise_xor.reduce(u_out))
-        idx = vals_out.astype(np.int64) if op == "pairs" else None
-        if op == "pairs":
-            ok &= bool(np.array_equal(keys_in[idx], keys_out))
-    ok &= bool(np.all(o[1:] >= o[:-1]))
-    if idx is not None:
-        tie = o[1:] == o[:-1]
-        ok &= bool(np.all(idx[1:][tie] > idx[:-1][tie]))
-    return ok
+        return bool(np.array_equal(vals_out, idx))
+    return bool(np.array_equal(ordered_bits(keys_out), o[idx]) and np.array_equal(vals_out, vals_in[idx]))
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(keys, seconds):
-    """Oracle ('port', 1 core) on the full input, repeated for ~`seconds`;
-    C++ stand-ins once each on the same input."""
+# The GPU box grants one GPU's share of its host (16 threads, whatever nproc
+# shows there); a parallel CPU sort is run on at most that many threads.
+BOX_CPU_SHARE = 16
+
+
+def cpu_baseline(keys, seconds, gpu_out):
+    """Oracle ('port', 1 core) on the full input, repeated for ~`seconds`,
+    its first output compared bit for bit with the GPU's (`gpu_out`); C++
+    stand-ins once each on the same input."""
     import oracle
     n = keys.size
     runs = []
+    oracle_match = None
     t_end = time.perf_counter() + seconds
     while True:
         t0 = time.perf_counter()
         out = oracle.sort("u32", keys)
         runs.append(time.perf_counter() - t0)
+        if oracle_match is None:
+            oracle_match = bool(np.array_equal(out, gpu_out))
         del out
         if time.perf_counter() >= t_end:
             break
     port = n / float(np.median(runs)) / 1e6
+    affinity = len(os.sched_getaffinity(0))
     res = {"value": round(port, 1), "unit": "Mkeys/s", "cores": 1, "kind": "port",
            "sample": f"oracle C radix sort (MSD byte 3 + per-bucket LSD bytes 0-2) on the same "
                      f"{n:,} keys, {len(runs)} run(s), median",
-           "cpu_model": _cpu_model()}
+           "oracle_match": oracle_match,
+           "cpu_model": _cpu_model(), "nproc": os.cpu_count(), "affinity_cpus": affinity}
     try:
         lib = ctypes.CDLL(os.path.join(ROOT, "oracle", "_build", "libcpubase.so"))
         lib.cb_std_sort_u32.argtypes = [ctypes.c_void_p, ctypes.c_uint64]
         lib.cb_parallel_sort_u32.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int]
-        threads = min(16, os.cpu_count() or 1)
+        threads = max(1, min(BOX_CPU_SHARE, affinity))
         a = keys.copy()
         t0 = time.perf_counter()
         lib.cb_std_sort_u32(a.ctypes.data, n)
@@ -174,7 +174,9 @@ def cpu_baseline(keys, seconds):
             "std_sort": {"value": round(n / t_std / 1e6, 1), "cores": 1,
                          "stands_in_for": "Rust slice::sort_unstable"},
             "gnu_parallel_sort": {"value": round(n / t_par / 1e6, 1), "cores": threads,
-                                  "stands_in_for": "rayon par_sort_unstable"},
+                                  "stands_in_for": "rayon par_sort_unstable",
+                                  "thread_limit": f"min(affinity CPUs {affinity}, the GPU box's per-GPU "
+                                                  f"share {BOX_CPU_SHARE}); nproc {os.cpu_count()}"},
         }
     except OSError as e:
         log(f"cpu stand-ins unavailable: {e}")
@@ -182,13 +184,23 @@ def cpu_baseline(keys, seconds):
 
 
 def _cpu_model():
+    """/proc/cpuinfo's model name, with family/model/stepping (the name alone
+    can be as short as "AMD EPYC")."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                if k in ("model name", "cpu family", "model", "stepping") and k not in info:
+                    info[k] = v
+            if not line.strip() and info:
+                break
     except OSError:
-        pass
-    return None
+        return None
+    if not info:
+        return None
+    return (f"{info.get('model name', '?')} (family {info.get('cpu family', '?')}, "
+            f"model {info.get('model', '?')}, stepping {info.get('stepping', '?')})")
 
 
 def load_traffic():
@@ -278,15 +290,17 @@ def main():
     if vbufs:
         vbufs[-1].set_len(n)
         vals_out = vbufs[-1].as_slice()
-    ok = check_output(op_name, keys, vals, keys_out, vals_out)
-    del keys_out, vals_out
+    # exact output check: the oracle's sort of the same keys in the cpu_baseline
+    # leg of the headline line, numpy's otherwise
+    check_with_oracle = headline and not args.no_cpu_baseline
+    exact = None if check_with_oracle else check_output(op_name, keys, vals, keys_out, vals_out)
     for b in bufs + vbufs:
         b.free()
     src.free()
     if vsrc is not None:
         vsrc.free()
-    if not ok:
-        print("bench: output check FAILED", file=sys.stderr)
+    if exact is False:
+        print("bench: output check FAILED (timed output differs from the exact sort)", file=sys.stderr)
         sys.exit(3)
 
     ms_per_step = (t1 - t0) * 1e3 / K
@@ -345,7 +359,11 @@ def main():
     cpu = None
     if headline and not args.no_cpu_baseline:
         log("bench: cpu baseline")
-        cpu = cpu_baseline(keys, args.cpu_seconds)
+        cpu = cpu_baseline(keys, args.cpu_seconds, keys_out)
+        if not cpu["oracle_match"]:
+            print("bench: timed output differs from the oracle's sort", file=sys.stderr)
+            sys.exit(3)
+    del keys_out, vals_out
 
     api = {"sort": "sort_buffer", "argsort": "argsort (device buffers)",
            "pairs": "sort_pairs (device buffers)"}[op_name]
@@ -363,6 +381,8 @@ def main():
         "roofline": roofline,
         "sort_roofline": {"bytes_per_key": sort_bytes, "frac": round(sort_frac, 4),
                           "achieved_GBps": round(sort_frac * HBM_PEAK_GBS, 1)},
+        "oracle_match": cpu["oracle_match"] if cpu else None,
+        "exact_match": cpu["oracle_match"] if cpu else exact,
         "kernels": kernels, "kernel_ms_per_step": round(kernel_sum_ms, 4),
         "slice_api": slice_api,
         "cpu_baseline": cpu,

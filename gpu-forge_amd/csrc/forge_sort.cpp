@@ -67,6 +67,14 @@ struct fs_sorter {
 
     hipStream_t last_stream = nullptr;   // stream of the last enqueued sort
     bool pending = false;
+    // A sort was enqueued on a capturing stream: a HIP graph may hold the
+    // addresses of the scratch buffers, so they must not be reallocated.
+    bool captured = false;
+
+    // Test options (fs_sorter_set_test_option); defaults give the product layout.
+    bool force_wide = false;             // 64-bit look-back entries for any n
+    uint32_t up_blocks_per_cu = 0;       // upsweep blocks per CU (0: by key width)
+    uint32_t fault = FS_FAULT_NONE;      // injected fault (FS_FAULT_INJECTION builds only)
 
     bool profiling = false;
     std::vector<ProfEntry> prof;         // launches since profiling was enabled or reset
@@ -160,8 +168,15 @@ static fs_status drain(fs_sorter* s) {
 
 // Grow-only device buffer (ensure_buffers*, lib.rs:1120-1289).  Growing waits
 // for in-flight work first, since that work may still use the old buffer.
-static fs_status ensure(fs_sorter* s, DevBuf& b, size_t bytes) {
+// graph_visible: kernels a caller may capture use the buffer (everything but
+// the slice API's staging buffers, which only synchronous calls use).
+static fs_status ensure(fs_sorter* s, DevBuf& b, size_t bytes, bool graph_visible = true) {
     if (b.bytes >= bytes) return FS_OK;
+    if (s->captured && graph_visible)
+        return set_err(s, FS_ERR_INVALID_ARGUMENT,
+                       "scratch must grow to %zu bytes, but a sort of this sorter was captured into a HIP graph that "
+                       "may still use it: reserve capacity (fs_reserve) before capturing, or call "
+                       "fs_allow_scratch_growth once those graphs are destroyed", bytes);
     fs_status st = drain(s);
     if (st != FS_OK) return st;
     free_buf(b);
@@ -212,12 +227,24 @@ static fs_status launch(fs_sorter* s, int k, unsigned grid, unsigned block, void
     return FS_OK;
 }
 
+// After a device error the histogram and the schedule (with the upsweep's
+// ticket) are cleared, so the next sort starts from the state every sort
+// leaves behind.  The device is idle here (the caller has synchronised).
+static void reset_device_tables(fs_sorter* s) {
+    (void)hipMemset(s->hist, 0, (size_t)FS_MAX_DIGITS * FS_RADIX * 4);
+    (void)hipMemset(s->plan, 0, FS_PLAN_WORDS * sizeof(uint32_t));
+    (void)hipDeviceSynchronize();
+}
+
 static fs_status check_device_status(fs_sorter* s) {
     uint32_t st = __atomic_load_n(s->status, __ATOMIC_ACQUIRE);
     if (st) {
         __atomic_store_n(s->status, 0u, __ATOMIC_RELEASE);
+        reset_device_tables(s);
         if (st & FS_DEVERR_BAD_TILE)
             return set_err(s, FS_ERR_GPU_EXECUTION, "digit pass drew a tile id beyond the grid");
+        if (st & FS_DEVERR_BAD_DIGITS)
+            return set_err(s, FS_ERR_GPU_EXECUTION, "digit count does not match the key width");
         if (st & FS_DEVERR_BAD_PLAN)
             return set_err(s, FS_ERR_GPU_EXECUTION, "device schedule named an unknown buffer");
         if (st & FS_DEVERR_LOOKBACK_TIMEOUT)
@@ -230,6 +257,36 @@ static fs_status check_device_status(fs_sorter* s) {
 // ---------------------------------------------------------------------------
 // the launch sequence
 // ---------------------------------------------------------------------------
+
+static int variant_of(fs_op op, fs_key_type t) {
+    return key64(t) ? (op == FS_OP_SORT ? FS_VAR_K64 : FS_VAR_K64V) : (op == FS_OP_SORT ? FS_VAR_K32 : FS_VAR_K32V);
+}
+
+// Look-back tile entries are 64-bit once an inclusive prefix may need more
+// than 30 bits, or when a test forces that layout.
+static bool wide_lookback(const fs_sorter* s, uint64_t n) { return n >= FS_LB_WIDE_KEYS || s->force_wide; }
+
+// Grows the scratch a sort of n keys needs (grow-only, like ensure_buffers*,
+// lib.rs:1120-1289): ping-pong buffers for keys (and values), and two
+// look-back arrays of tile entries followed by one 32-bit group entry per
+// FS_LB_GROUP tiles.
+static fs_status reserve(fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
+    if (n <= 1) return FS_OK;
+    const size_t kb = key_bytes(t);
+    const uint32_t tile = s->tile[variant_of(op, t)];
+    const uint64_t num_tiles = (n + tile - 1) / tile;
+    fs_status r;
+    if ((r = ensure(s, s->s1k, n * kb)) != FS_OK) return r;
+    if ((r = ensure(s, s->s2k, n * kb)) != FS_OK) return r;
+    if (op != FS_OP_SORT) {
+        if ((r = ensure(s, s->s1v, n * 4)) != FS_OK) return r;
+        if (op == FS_OP_PAIRS && (r = ensure(s, s->s2v, n * 4)) != FS_OK) return r;
+    }
+    const size_t lb_bytes = (size_t)num_tiles * FS_RADIX * (wide_lookback(s, n) ? 8 : 4) +
+                            (size_t)((num_tiles + FS_LB_GROUP - 1) / FS_LB_GROUP) * FS_RADIX * 4;
+    if ((r = ensure(s, s->lb0, lb_bytes)) != FS_OK) return r;
+    return ensure(s, s->lb1, lb_bytes);
+}
 
 static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint32_t* vals,
                          uint64_t n, hipStream_t st) {
@@ -255,27 +312,12 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     const size_t kb = key_bytes(t);
     if ((uintptr_t)keys % kb != 0 || (vals && (uintptr_t)vals % 4 != 0))
         return set_err(s, FS_ERR_INVALID_ARGUMENT, "misaligned key or value pointer");
-    const int var = key64(t) ? (op == FS_OP_SORT ? FS_VAR_K64 : FS_VAR_K64V)
-                             : (op == FS_OP_SORT ? FS_VAR_K32 : FS_VAR_K32V);
+    const int var = variant_of(op, t);
     const uint32_t tile = s->tile[var];
     const uint32_t num_tiles = (uint32_t)((n + tile - 1) / tile);
+    const bool wide = wide_lookback(s, n);
     fs_status r;
-    if ((r = ensure(s, s->s1k, n * kb)) != FS_OK) return r;
-    if ((r = ensure(s, s->s2k, n * kb)) != FS_OK) return r;
-    if (op != FS_OP_SORT) {
-        if ((r = ensure(s, s->s1v, n * 4)) != FS_OK) return r;
-        if (op == FS_OP_PAIRS && (r = ensure(s, s->s2v, n * 4)) != FS_OK) return r;
-    }
-    // Look-back arrays: tile entries (64-bit once an inclusive prefix may need
-    // more than 30 bits), then one 32-bit group entry per FS_LB_GROUP tiles.
-    // FS_LB_FORCE_WIDE=1 selects the 64-bit entries for any n (a test switch
-    // for that layout).
-    const char* force_wide = getenv("FS_LB_FORCE_WIDE");
-    const bool wide = n >= FS_LB_WIDE_KEYS || (force_wide && force_wide[0] == '1');
-    const size_t lb_bytes = (size_t)num_tiles * FS_RADIX * (wide ? 8 : 4) +
-                            (size_t)((num_tiles + FS_LB_GROUP - 1) / FS_LB_GROUP) * FS_RADIX * 4;
-    if ((r = ensure(s, s->lb0, lb_bytes)) != FS_OK) return r;
-    if ((r = ensure(s, s->lb1, lb_bytes)) != FS_OK) return r;
+    if ((r = reserve(s, op, t, n)) != FS_OK) return r;
 
     FsArgs a;
     memset(&a, 0, sizeof a);
@@ -292,10 +334,8 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     // counter clears, folds and histogram atomics for the same keys), 2 for
     // 64-bit keys (the blocks' 64 KiB of counters allow two resident); fewer
     // when the keys give each block less than one step of FS_UPSWEEP_UNROLL
-    // units per thread; FS_UPSWEEP_BLOCKS_PER_CU overrides
-    static const uint32_t up_env = getenv("FS_UPSWEEP_BLOCKS_PER_CU")
-                                       ? (uint32_t)atoi(getenv("FS_UPSWEEP_BLOCKS_PER_CU")) : 0u;
-    const uint64_t up_per_cu = up_env ? up_env : (key64(t) ? 2u : 1u);
+    // units per thread (a test option can set the blocks per CU)
+    const uint64_t up_per_cu = s->up_blocks_per_cu ? s->up_blocks_per_cu : (key64(t) ? 2u : 1u);
     const uint64_t up_units = a.vec_ok ? n / (16u / key_bytes(t)) : n;
     const uint64_t up_span = (uint64_t)FS_UPSWEEP_UNROLL * FS_HIST_BLOCK;
     uint64_t up_blocks = (up_units + up_span - 1) / up_span;
@@ -314,6 +354,10 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.plan = (uint64_t)(uintptr_t)s->plan;
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
+#ifdef FS_FAULT_INJECTION
+    a.fault = s->fault;
+    if (s->fault == FS_FAULT_BAD_DIGITS) a.digits = 5u;
+#endif
 
     const unsigned up_grid = (unsigned)up_blocks;
     void* args1[] = {&a};
@@ -325,7 +369,11 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         // digit 0 of a keys-only sort: its pass, when it runs, is the first,
         // which needs no stability (same tiles as the stable kernel)
         const int k = (d == 0 && op == FS_OP_SORT) ? (key64(t) ? K_ANY64 : K_ANY32) : os;
-        if ((r = launch(s, k, num_tiles, s->block[var], args2, st)) != FS_OK) return r;
+        unsigned grid = num_tiles;
+#ifdef FS_FAULT_INJECTION
+        if (s->fault == FS_FAULT_EXTRA_BLOCK && d == 0) grid += 1u;
+#endif
+        if ((r = launch(s, k, grid, s->block[var], args2, st)) != FS_OK) return r;
     }
     s->last_stream = st;
     s->pending = true;
@@ -547,11 +595,62 @@ fs_status fs_encode(fs_sorter* s, fs_op op, fs_key_type type, void* device_keys,
     if (!s) return FS_ERR_INVALID_ARGUMENT;
     HIP_TRY(s, hipSetDevice(s->device));
     hipStream_t st = hip_stream ? (hipStream_t)hip_stream : s->stream;
-    if (s->pending && s->last_stream != st) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
+        (void)hipGetLastError();
+        cap = hipStreamCaptureStatusNone;
+    }
+    if (cap == hipStreamCaptureStatusActive) {
+        // The graph being captured will hold the scratch addresses: from now
+        // on the scratch may not be reallocated (ensure refuses to grow it,
+        // including for this sort, which must fit what was reserved).
+        s->captured = true;
+    } else if (s->pending && s->last_stream != st) {
         fs_status r = drain(s);   // scratch is shared: serialise sorts issued on different streams
         if (r != FS_OK) return r;
     }
     return enqueue(s, op, type, device_keys, op == FS_OP_SORT ? nullptr : device_values, n, st);
+}
+
+fs_status fs_reserve(fs_sorter* s, fs_op op, fs_key_type type, uint64_t n) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    if (!valid_type(type)) return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown key type %d", (int)type);
+    if (op != FS_OP_SORT && op != FS_OP_ARGSORT && op != FS_OP_PAIRS)
+        return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown op %d", (int)op);
+    if (n >= (1ull << 32))
+        return set_err(s, FS_ERR_INVALID_ARGUMENT, "n = %llu exceeds 2^32 - 1", (unsigned long long)n);
+    HIP_TRY(s, hipSetDevice(s->device));
+    return reserve(s, op, type, n);
+}
+
+fs_status fs_allow_scratch_growth(fs_sorter* s) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    s->captured = false;
+    return FS_OK;
+}
+
+fs_status fs_sorter_set_test_option(fs_sorter* s, fs_test_option opt, uint64_t value) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    switch (opt) {
+        case FS_TEST_WIDE_LOOKBACK: s->force_wide = value != 0; return FS_OK;
+        case FS_TEST_UPSWEEP_BLOCKS_PER_CU:
+            if (value > 64) return set_err(s, FS_ERR_INVALID_ARGUMENT, "upsweep blocks per CU %llu > 64",
+                                           (unsigned long long)value);
+            s->up_blocks_per_cu = (uint32_t)value;
+            return FS_OK;
+        case FS_TEST_INJECT_FAULT:
+#ifdef FS_FAULT_INJECTION
+            if (value > FS_FAULT_STALL_TILE) return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown fault %llu",
+                                                           (unsigned long long)value);
+            s->fault = (uint32_t)value;
+            return FS_OK;
+#else
+            return set_err(s, FS_ERR_INVALID_ARGUMENT, "fault injection is not compiled into this library");
+#endif
+    }
+    return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown test option %d", (int)opt);
 }
 
 fs_status fs_synchronize(fs_sorter* s) {
@@ -651,8 +750,8 @@ static fs_status host_op(fs_sorter* s, fs_op op, fs_key_type type, void* keys, u
     fs_status r = drain(s);
     if (r != FS_OK) return r;
     const size_t kb = key_bytes(type);
-    if ((r = ensure(s, s->iok, n * kb)) != FS_OK) return r;
-    if (op != FS_OP_SORT && (r = ensure(s, s->iov, n * 4)) != FS_OK) return r;
+    if ((r = ensure(s, s->iok, n * kb, false)) != FS_OK) return r;
+    if (op != FS_OP_SORT && (r = ensure(s, s->iov, n * 4, false)) != FS_OK) return r;
     if ((r = ensure_pinned(s)) != FS_OK) return r;
     if ((r = stage_to_device(s, s->iok.p, keys, n * kb)) != FS_OK) return r;
     if (op == FS_OP_PAIRS && (r = stage_to_device(s, s->iov.p, vals, n * 4)) != FS_OK) return r;

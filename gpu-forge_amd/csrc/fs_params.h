@@ -117,8 +117,11 @@
 
 // Bounded spin of a look-back wait (iterations of s_sleep(1), ~64 clocks each).
 // A predecessor tile that owns a tile id is resident and finishes in
-// microseconds; the bound only guarantees that every wait ends.
+// microseconds; the bound only guarantees that every wait ends.  (The CPU
+// emulator's fault-injection build sets a tiny bound.)
+#ifndef FS_SPIN_LIMIT
 #define FS_SPIN_LIMIT (1u << 24)
+#endif
 
 // Per-pass flags in the device-side schedule.
 #define FS_PASS_FIRST 1u   // apply the forward key transform on load; argsort: generate indices
@@ -166,6 +169,15 @@
 #define FS_DEVERR_BAD_TILE 2u        // a digit pass block mapped to a tile >= num_tiles
 #define FS_DEVERR_BAD_PLAN 4u        // a schedule named a buffer the call does not have
 #define FS_DEVERR_GATHER_INDEX 8u    // a gather index was >= the source length
+#define FS_DEVERR_BAD_DIGITS 16u     // the digit count does not match the key width
+
+// Faults a CPU-emulator test build (FS_FAULT_INJECTION) can inject, so that
+// every device-side guard is exercised without a faulty kernel on a GPU.
+#define FS_FAULT_NONE 0u
+#define FS_FAULT_BAD_DIGITS 1u     // host passes a digit count other than 4/8 -> BAD_PLAN
+#define FS_FAULT_BAD_BUFFER 2u     // schedule names an unknown buffer for the first pass -> BAD_PLAN
+#define FS_FAULT_EXTRA_BLOCK 3u    // first digit pass launched with one block too many -> BAD_TILE
+#define FS_FAULT_STALL_TILE 4u     // tile 1 of the first pass never publishes -> LOOKBACK_TIMEOUT
 
 // Kernel argument block, passed by value to every kernel.
 typedef struct FsArgs {
@@ -178,7 +190,7 @@ typedef struct FsArgs {
     uint32_t wide;              // 1: 64-bit look-back tile entries (n >= FS_LB_WIDE_KEYS)
     uint32_t tile;              // keys per tile of the digit-pass variant in use
     uint32_t vec_ok;            // keys pointer is 16-byte aligned
-    uint32_t pad2;
+    uint32_t fault;             // FS_FAULT_* to inject (read only by FS_FAULT_INJECTION builds), else 0
     uint64_t keys;              // caller keys (in place for KEYS/PAIRS; read-only for ARGSORT)
     uint64_t vals;              // caller values (PAIRS) or output indices (ARGSORT)
     uint64_t s1k, s2k, s1v, s2v;   // scratch ping-pong buffers

@@ -33,6 +33,9 @@ NP_DTYPES = {"u32": np.uint32, "i32": np.int32, "f32": np.float32,
              "u64": np.uint64, "i64": np.int64, "f64": np.float64}
 KEY_SIZE = {"u32": 4, "i32": 4, "f32": 4, "u64": 8, "i64": 8, "f64": 8}   # SortKey::KEY_SIZE
 OP_SORT, OP_ARGSORT, OP_PAIRS = 0, 1, 2
+# fs_test_option and the FS_FAULT_* codes (include/forge_sort.h, csrc/fs_params.h)
+TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT = 0, 1, 2
+FAULT_NONE, FAULT_BAD_DIGITS, FAULT_BAD_BUFFER, FAULT_EXTRA_BLOCK, FAULT_STALL_TILE = 0, 1, 2, 3, 4
 
 FS_OK = 0
 FS_ERR_DEVICE_NOT_FOUND = 1
@@ -121,6 +124,9 @@ def _load():
         "fs_argsort_buffer": ([vp, i, vp, u64, vp], i),
         "fs_sort_pairs_buffer": ([vp, i, vp, vp, u64], i),
         "fs_encode": ([vp, i, i, vp, vp, u64, vp], i),
+        "fs_reserve": ([vp, i, i, u64], i),
+        "fs_allow_scratch_growth": ([vp], i),
+        "fs_sorter_set_test_option": ([vp, i, u64], i),
         "fs_synchronize": ([vp], i),
         "fs_last_pass_info": ([vp, u32p, u32p], i),
         "fs_set_profiling": ([vp, i], i),
@@ -352,6 +358,21 @@ class GpuSorter:
 
     def synchronize(self):
         self._check(_load().fs_synchronize(self._h))
+
+    def reserve(self, op, kind, n):
+        """Grow the scratch for sorts of up to n keys (e.g. before capturing a
+        sort into a HIP graph, after which the scratch may not grow)."""
+        self._check(_load().fs_reserve(self._h, op, KEY_TYPES[kind], n))
+
+    def allow_scratch_growth(self):
+        """Every graph that captured a sort of this sorter has been destroyed."""
+        self._check(_load().fs_allow_scratch_growth(self._h))
+
+    def set_test_option(self, option, value):
+        """Testing hooks (TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU,
+        TEST_INJECT_FAULT): reach layouts the product uses only at sizes too
+        large for a test, or inject a device-side fault (emulator builds)."""
+        self._check(_load().fs_sorter_set_test_option(self._h, option, value))
 
     def device_synchronize(self):
         """Wait for everything on the device (hipDeviceSynchronize)."""

@@ -137,9 +137,29 @@ fs_status fs_sort_pairs_buffer(fs_sorter *s, fs_key_type type, void *device_keys
  * the sort on `hip_stream` (NULL = the sorter's stream) and return without
  * waiting.  For FS_OP_ARGSORT `device_values` is the index output and
  * `device_keys` is read only; for FS_OP_SORT `device_values` is ignored.
- * Errors detected on the device are reported by the next fs_synchronize. */
+ * Errors detected on the device are reported by the next fs_synchronize.
+ *
+ * HIP graph capture: fs_encode on a capturing stream records kernel launches
+ * only (no memset, no allocation).  The graph then holds the addresses of the
+ * sorter's scratch (ping-pong buffers, look-back arrays, histogram, schedule),
+ * so from that call on the sorter refuses to grow its scratch
+ * (FS_ERR_INVALID_ARGUMENT), the captured sort included: reserve capacity with
+ * fs_reserve before capturing.  Graphs must be destroyed before
+ * fs_sorter_free, and fs_allow_scratch_growth re-enables growth once they are.
+ * A replay uses the same scratch as the sorter's eager sorts: launch replays
+ * on the sorter's stream (or order them with its other work). */
 fs_status fs_encode(fs_sorter *s, fs_op op, fs_key_type type, void *device_keys,
                     uint32_t *device_values, uint64_t n, void *hip_stream);
+
+/* Grow the sorter's scratch for sorts of up to n keys of `type` with `op`
+ * (the grow-only ensure_buffers*, lib.rs:1120-1289, done ahead of time), e.g.
+ * before capturing a sort into a HIP graph.  Synchronous. */
+fs_status fs_reserve(fs_sorter *s, fs_op op, fs_key_type type, uint64_t n);
+
+/* Lift the no-growth rule a captured sort imposes (see fs_encode); call only
+ * once every graph that captured a sort of this sorter has been destroyed.
+ * No counterpart in the reference (Metal has no graph capture). */
+fs_status fs_allow_scratch_growth(fs_sorter *s);
 
 /* Wait for the sorter's stream (and the last encode's stream); report device errors. */
 fs_status fs_synchronize(fs_sorter *s);
@@ -173,6 +193,19 @@ fs_status fs_read_lookback_stats(fs_sorter *s, uint64_t counters[4]);
 /* Keys per tile of the digit-pass kernels compiled into the loaded code
  * object: [u32 keys, u32 keys + values, u64 keys, u64 keys + values]. */
 fs_status fs_tile_config(const fs_sorter *s, uint32_t keys_per_tile[4]);
+
+/* ---- testing hooks (no counterpart in the reference) ---------------------------
+ * Layout switches that let tests reach code paths the product takes only at
+ * sizes too large for a test, and (in CPU-emulator builds compiled with
+ * FS_FAULT_INJECTION only) injected faults that drive the device-side error
+ * guards.  The product never reads the environment for these; the defaults
+ * give the normal layout.  Not for production use. */
+typedef enum fs_test_option {
+    FS_TEST_WIDE_LOOKBACK = 0,          /* value != 0: 64-bit look-back entries for any n */
+    FS_TEST_UPSWEEP_BLOCKS_PER_CU = 1,  /* histogram blocks per CU, 1..64 (0 = by key width) */
+    FS_TEST_INJECT_FAULT = 2            /* FS_FAULT_* (fault-injection builds only) */
+} fs_test_option;
+fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t value);
 
 /* ---- GpuGather (forge-runtime/src/gather.rs:26-173) --------------------------
  * output[i] = source[indices[i]] for u32 or u64 elements, u32 indices

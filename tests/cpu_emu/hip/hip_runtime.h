@@ -173,6 +173,11 @@ hipError_t hipDeviceGetAttribute(int*, hipDeviceAttribute_t, int);
 hipError_t hipGetLastError(void);
 const char* hipGetErrorString(hipError_t);
 hipError_t hipStreamCreateWithFlags(hipStream_t*, unsigned);
+typedef enum { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1,
+               hipStreamCaptureStatusInvalidated = 2 } hipStreamCaptureStatus;
+hipError_t hipStreamBeginCapture(hipStream_t, int);
+hipError_t hipStreamEndCapture(hipStream_t, void**);
+hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus*);
 hipError_t hipStreamDestroy(hipStream_t);
 hipError_t hipStreamSynchronize(hipStream_t);
 hipError_t hipDeviceSynchronize(void);

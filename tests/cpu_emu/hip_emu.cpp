@@ -264,6 +264,11 @@ void launch(const char* name, void (*entry)(void**), uint32_t grid, uint32_t blo
     g_kernel = name;
     if (getenv("EMU_TRACE")) fprintf(stderr, "hip_emu: launch %s grid=%u block=%u\n", name, grid, block);
     const int nx = xcds();
+    int hold_queue = -1, hold_ms = 0;
+    static std::atomic<bool> held{false};
+    if (const char* h = getenv("EMU_HOLD_QUEUE"))
+        if (strncmp(name, "fs_onesweep", 11) == 0 && !held.exchange(true) && sscanf(h, "%d:%d", &hold_queue, &hold_ms) != 2)
+            hold_ms = 0;
     std::vector<std::atomic<uint32_t>> next(nx);           // per-queue position
     for (auto& c : next) c = 0;
     auto worker = [&](int queue) {
@@ -274,6 +279,10 @@ void launch(const char* name, void (*entry)(void**), uint32_t grid, uint32_t blo
             ss.ss_flags = 0;
             sigaltstack(&ss, nullptr);
         }
+        // EMU_HOLD_QUEUE=q:ms holds queue q of every digit-pass launch back for
+        // ms milliseconds, as if another stream's work occupied that XCD
+        // (the first digit-pass launch of the process only)
+        if (hold_ms > 0 && queue == hold_queue) std::this_thread::sleep_for(std::chrono::milliseconds(hold_ms));
         for (;;) {
             const uint64_t b = (uint64_t)queue + (uint64_t)nx * next[queue].fetch_add(1);
             if (b >= grid) break;
@@ -331,7 +340,7 @@ static emu_function g_funcs[] = {
 };
 
 struct emu_module { int dummy; };
-struct emu_stream { int dummy; };
+struct emu_stream { bool capturing = false; };
 struct emu_event { std::chrono::steady_clock::time_point t; };
 
 // ---------------------------------------------------------------------------
@@ -428,6 +437,24 @@ hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
 hipError_t hipGetLastError(void) { return hipSuccess; }
 const char* hipGetErrorString(hipError_t e) { return e == hipSuccess ? "success" : "emulated HIP error"; }
 hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned) { *s = new emu_stream(); return hipSuccess; }
+// Capture is a state flag only: launches on a capturing stream still run at
+// once (enough for the host runtime's capture rules, which is what the
+// emulator tests); the default stream (nullptr) never captures.
+hipError_t hipStreamBeginCapture(hipStream_t s, int) {
+    if (!s) return hipErrorInvalidValue;
+    s->capturing = true;
+    return hipSuccess;
+}
+hipError_t hipStreamEndCapture(hipStream_t s, void** graph) {
+    if (!s || !s->capturing) return hipErrorInvalidValue;
+    s->capturing = false;
+    if (graph) *graph = nullptr;
+    return hipSuccess;
+}
+hipError_t hipStreamIsCapturing(hipStream_t s, hipStreamCaptureStatus* st) {
+    *st = (s && s->capturing) ? hipStreamCaptureStatusActive : hipStreamCaptureStatusNone;
+    return hipSuccess;
+}
 hipError_t hipStreamDestroy(hipStream_t s) { delete s; return hipSuccess; }
 hipError_t hipStreamSynchronize(hipStream_t) { flush_copies(); return hipSuccess; }
 hipError_t hipDeviceSynchronize(void) { flush_copies(); return hipSuccess; }
@@ -459,3 +486,8 @@ hipError_t hipEventElapsedTime(float* ms, hipEvent_t a, hipEvent_t b) {
     *ms = std::chrono::duration<float, std::milli>(b->t - a->t).count();
     return hipSuccess;
 }
+
+// Test helpers the emulator tests call through ctypes (TEST INFRASTRUCTURE).
+extern "C" void* emu_test_stream_create() { hipStream_t s = nullptr; hipStreamCreateWithFlags(&s, 0); return s; }
+extern "C" int emu_test_begin_capture(void* s) { return hipStreamBeginCapture((hipStream_t)s, 0); }
+extern "C" int emu_test_end_capture(void* s) { return hipStreamEndCapture((hipStream_t)s, nullptr); }

@@ -6,6 +6,7 @@ device memory fault (the guard pages turn it into SIGSEGV -> exit code 86)
 or an emulator deadlock cannot take the test runner down.  The forge_sort
 package is pointed at the emulation library only inside this process.
 """
+import ctypes
 import os
 import sys
 
@@ -96,7 +97,100 @@ def check_gather(kind, n, seed):
     return np.array_equal(out, oracle.gather(src, idx))
 
 
+# injected fault -> the message its device-side guard must report
+FAULTS = {
+    "fault_digits": (forge_sort.FAULT_BAD_DIGITS, "digit count does not match the key width"),
+    "fault_buffer": (forge_sort.FAULT_BAD_BUFFER, "device schedule named an unknown buffer"),
+    "fault_tile": (forge_sort.FAULT_EXTRA_BLOCK, "digit pass drew a tile id beyond the grid"),
+    "fault_stall": (forge_sort.FAULT_STALL_TILE, "look-back wait exceeded its spin bound"),
+}
+
+
+def sorted_ok(sorter, kind, keys):
+    got = keys.copy()
+    getattr(sorter, f"sort_{kind}")(got)
+    return np.array_equal(got.view(BITS[kind]), oracle.sort(kind, keys).view(BITS[kind]))
+
+
+def check_fault(sorter, op, kind, keys):
+    """The injected fault must come back as GpuExecution with its guard's
+    message; the next sort without the fault must be exact again."""
+    code, message = FAULTS[op]
+    sorter.set_test_option(forge_sort.TEST_INJECT_FAULT, code)
+    got = keys.copy()
+    try:
+        getattr(sorter, f"sort_{kind}")(got)
+        raised = None
+    except forge_sort.GpuExecution as e:
+        raised = str(e)
+    finally:
+        sorter.set_test_option(forge_sort.TEST_INJECT_FAULT, forge_sort.FAULT_NONE)
+    if raised is None or message not in raised:
+        print(f"  expected GpuExecution '{message}', got {raised!r}", flush=True)
+        return False
+    return sorted_ok(sorter, kind, keys)
+
+
+def check_timeout_or_exact(sorter, kind, keys):
+    """A digit pass whose XCD queue is held back (EMU_HOLD_QUEUE): either the
+    held tiles arrive within the spin bound and the sort is exact, or the
+    waits end at the bound with GpuExecution; then a sort is exact again."""
+    got = keys.copy()
+    try:
+        getattr(sorter, f"sort_{kind}")(got)
+        ok = np.array_equal(got.view(BITS[kind]), oracle.sort(kind, keys).view(BITS[kind]))
+        print("  held queue: completed", flush=True)
+    except forge_sort.GpuExecution as e:
+        ok = "look-back wait exceeded its spin bound" in str(e)
+        print(f"  held queue: {e}", flush=True)
+    return ok and sorted_ok(sorter, kind, keys)
+
+
+def check_capture(sorter, kind, n, seed):
+    """HIP-graph capture rules: a sort enqueued on a capturing stream may not
+    grow the scratch (fs_reserve first); after a capture no sort may grow it
+    until fs_allow_scratch_growth; sorts that fit keep working."""
+    L = forge_sort._load()
+    st = L.emu_test_stream_create
+    st.restype = ctypes.c_void_p
+    stream = st()
+    small, big = keys_for(kind, n, "uniform", seed), keys_for(kind, 3 * n, "uniform", seed + 1)
+    sorter.reserve(forge_sort.OP_SORT, kind, n)
+    buf = sorter.alloc_sort_buffer(kind, 3 * n)
+    buf.copy_from_slice(small)
+    ok = L.emu_test_begin_capture(ctypes.c_void_p(stream)) == 0
+    sorter.encode(forge_sort.OP_SORT, kind, buf.device_ptr(), None, n, stream=stream)   # fits the reserve
+    try:
+        sorter.encode(forge_sort.OP_SORT, kind, buf.device_ptr(), None, 3 * n, stream=stream)
+        ok = False
+        print("  growth while capturing was not refused", flush=True)
+    except forge_sort.InvalidArgument:
+        pass
+    ok &= L.emu_test_end_capture(ctypes.c_void_p(stream)) == 0
+    sorter.synchronize()
+    try:
+        sorted_ok(sorter, kind, big)
+        ok = False
+        print("  growth after a capture was not refused", flush=True)
+    except forge_sort.InvalidArgument:
+        pass
+    ok &= sorted_ok(sorter, kind, keys_for(kind, n // 2, "few", seed + 2))   # fits: still fine
+    sorter.allow_scratch_growth()
+    ok &= sorted_ok(sorter, kind, big)
+    buf.free()
+    return ok
+
+
 def check(sorter, op, kind, n, dist, seed):
+    if op in FAULTS or op in ("hold", "capture"):
+        if op == "capture":
+            ok = check_capture(sorter, kind, n, seed)
+        elif op == "hold":
+            ok = check_timeout_or_exact(sorter, kind, keys_for(kind, n, dist, seed))
+        else:
+            ok = check_fault(sorter, op, kind, keys_for(kind, n, dist, seed))
+        print(f"{'PASS' if ok else 'FAIL'} {op} {kind} n={n}", flush=True)
+        return ok
     if op == "gather":
         ok = check_gather(kind, n, seed)
         print(f"{'PASS' if ok else 'FAIL'} gather {kind} n={n}", flush=True)
@@ -127,6 +221,11 @@ def main():
     flavor = sys.argv[1]
     use_emulator(flavor)
     sorter = forge_sort.GpuSorter.new()
+    # layout switches for the cases (testing hooks of the C ABI)
+    if os.environ.get("EMU_TEST_WIDE_LOOKBACK") == "1":
+        sorter.set_test_option(forge_sort.TEST_WIDE_LOOKBACK, 1)
+    if os.environ.get("EMU_TEST_UPSWEEP_PER_CU"):
+        sorter.set_test_option(forge_sort.TEST_UPSWEEP_BLOCKS_PER_CU, int(os.environ["EMU_TEST_UPSWEEP_PER_CU"]))
     print("tiles", sorter.tile_config(), flush=True)
     ok = True
     for spec in sys.argv[2:]:

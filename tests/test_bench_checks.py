@@ -76,3 +76,13 @@ def test_ordered_bits_total_order():
     v = np.concatenate([b.view(np.float32), nan_pos])
     o = bench.ordered_bits(v)
     assert np.all(o[1:] > o[:-1])
+
+
+def test_rejects_sum_and_xor_preserving_change():
+    """{1, 2} -> {0, 3} keeps the sum and the xor of the keys (a multiset test
+    by those two would pass it); the exact check must not."""
+    keys = np.array([2, 1, 7, 5], dtype=np.uint32)
+    wrong = np.array([0, 3, 5, 7], dtype=np.uint32)
+    assert int(keys.sum()) == int(wrong.sum()) and np.bitwise_xor.reduce(keys) == np.bitwise_xor.reduce(wrong)
+    assert not bench.check_output("sort", keys, None, wrong, None)
+    assert bench.check_output("sort", keys, None, np.sort(keys), None)

@@ -26,7 +26,7 @@ pytestmark = pytest.mark.skipif(shutil.which("g++") is None or shutil.which("mak
 
 @pytest.fixture(scope="module")
 def emulator():
-    r = subprocess.run(["make", "-C", EMU, "-j2"], capture_output=True, text=True, timeout=600)
+    r = subprocess.run(["make", "-C", EMU, "-j4"], capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stdout + r.stderr
     return EMU
 
@@ -98,10 +98,10 @@ def test_emulated_lookback_groups(emulator):
 @pytest.mark.parametrize("flavor", ["small", "groups"])
 def test_emulated_wide_lookback_entries(emulator, flavor):
     """The 64-bit look-back tile entries used from n = 2^30 on, forced for
-    small inputs (FS_LB_FORCE_WIDE=1)."""
+    small inputs (the FS_TEST_WIDE_LOOKBACK testing hook)."""
     run_cases(flavor, ["sort:u32:70000:uniform:2", "sort:i64:9000:uniform:3", "argsort:f32:33333:few:4",
                        "pairs:u64:5000:low12:5", "pairs:u32:40000:uniform:7"],
-              env={"EMU_CUS": "8", "FS_LB_FORCE_WIDE": "1"})
+              env={"EMU_CUS": "8", "EMU_TEST_WIDE_LOOKBACK": "1"})
 
 
 def test_emulated_upsweep_long_segments(emulator):
@@ -113,7 +113,7 @@ def test_emulated_upsweep_long_segments(emulator):
              "sort:i64:70001:uniform:4", "offset:u32:100003:uniform:5", "offset:u64:50001:few:6",
              "offset:f32:3:uniform:7"]
     for flavor in ("small", "prod"):
-        run_cases(flavor, cases, env={"EMU_CUS": "1", "FS_UPSWEEP_BLOCKS_PER_CU": "1"})
+        run_cases(flavor, cases, env={"EMU_CUS": "1", "EMU_TEST_UPSWEEP_PER_CU": "1"})
 
 
 def test_emulated_single_dispatch_queue(emulator):
@@ -123,3 +123,45 @@ def test_emulated_single_dispatch_queue(emulator):
     resident blocks allow."""
     run_cases("small", ["sort:u32:70000:uniform:2", "pairs:u32:40000:uniform:7", "sort:u64:9000:uniform:3"],
               env={"EMU_XCDS": "1", "EMU_WORKERS": "72"})
+
+
+def test_emulated_device_error_guards(emulator):
+    """Each device-side guard, driven by a fault injected in the emulator's
+    fault-injection build (never on a GPU), is reported as GpuExecution with
+    its own message, and the next sort is exact again: a digit count that does
+    not match the key width, a schedule naming an unknown buffer, a digit-pass
+    block beyond the tile grid, and a tile that never publishes (its
+    successors' look-back waits end at the build's tiny spin bound)."""
+    run_cases("faults", ["fault_digits:u32:5000:uniform:1", "fault_digits:u64:3000:uniform:2",
+                         "fault_buffer:u32:5000:uniform:3", "fault_buffer:i64:3000:uniform:4",
+                         "fault_tile:u32:5000:uniform:5", "fault_tile:f64:3000:uniform:6",
+                         "fault_stall:u32:9000:uniform:7", "fault_stall:u64:5000:uniform:8"],
+              env={"EMU_CUS": "8"})
+
+
+def test_emulated_held_xcd_queue(emulator):
+    """One XCD queue of the first digit pass held back for a second (another
+    stream's work on that XCD): the look-back waits on its tiles end at the
+    spin bound with a clean GpuExecution, or the sort completes exactly; then
+    a sort is exact again."""
+    run_cases("faults", ["hold:u32:40000:uniform:1"], env={"EMU_CUS": "8", "EMU_HOLD_QUEUE": "3:1000"})
+
+
+def test_emulated_capture_rules(emulator):
+    """A sort enqueued on a capturing stream fits the reserved scratch or is
+    refused; after a capture, growth is refused until fs_allow_scratch_growth."""
+    run_cases("small", ["capture:u32:3000:uniform:1", "capture:f64:2000:uniform:2"])
+
+
+def test_emulated_sanitizers(emulator):
+    """The product kernels and host runtime under AddressSanitizer and
+    UndefinedBehaviorSanitizer (host build of the emulator, libasan preloaded)."""
+    libasan = subprocess.run(["g++", "-print-file-name=libasan.so"], capture_output=True, text=True).stdout.strip()
+    if not os.path.isabs(libasan):
+        pytest.skip("libasan not found")
+    # ASan reports its own faults: the emulator's guard-page handler stays off
+    run_cases("san", ["sort:u32:5000:uniform:1", "sort:f32:3001:uniform:3", "argsort:i32:2000:few:7",
+                      "pairs:f64:2500:uniform:12", "sort:u32:5000:byte0:31", "sort:u32:9000:zipf:28",
+                      "gather:u32:3000:uniform:26"],
+              timeout=600, env={"LD_PRELOAD": libasan, "EMU_NO_SEGV_HANDLER": "1", "EMU_CUS": "4",
+                                "ASAN_OPTIONS": "detect_leaks=0:detect_stack_use_after_return=0"})

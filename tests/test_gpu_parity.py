@@ -333,12 +333,13 @@ def test_config4_64bit(sorter, kind):
 
 
 @pytest.fixture
-def force_wide_lookback():
+def force_wide_lookback(sorter):
     """Select the 64-bit look-back tile entries (normally used from n = 2^30
-    on) for every sort of the test; the library reads the switch per call."""
-    os.environ["FS_LB_FORCE_WIDE"] = "1"
+    on) for every sort of the test, through the sorter's testing hook."""
+    from forge_sort import TEST_WIDE_LOOKBACK
+    sorter.set_test_option(TEST_WIDE_LOOKBACK, 1)
     yield
-    del os.environ["FS_LB_FORCE_WIDE"]
+    sorter.set_test_option(TEST_WIDE_LOOKBACK, 0)
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -686,3 +687,72 @@ def test_gather_with_context_caller_stream(hip_stream):
         assert np.array_equal(gpu_gather(g, src, idx), src[idx])
     finally:
         g.close()
+
+
+# ---- callers of the path (forge-runtime pipelines, gpu-search) --------------------
+
+def test_device_argsort_gather_handoff_one_stream(hip_stream):
+    """forge-runtime's filter -> sort -> gather hand-off (buffer.rs:70-92,
+    pipeline.rs:98-105, gather.rs:81-119), entirely on the device and on one
+    caller stream: the argsort's index buffer leaves its SortBuffer through
+    into_raw_parts, is re-owned through from_raw_parts and feeds GpuGather's
+    encode directly; the host waits once, at the end.  The gathered column
+    must equal the payload in the stable order of the keys."""
+    from forge_sort import OP_ARGSORT, GpuGather, GpuSorter, SortBuffer
+    s = GpuSorter.with_context(0, hip_stream)
+    ga = GpuGather.with_context(0, hip_stream)
+    try:
+        for n, seed in ((1_000_003, 60), (16_777_216, 61)):
+            g = np.random.Generator(np.random.PCG64(seed))
+            keys = g.integers(0, 50_000, size=n, dtype=np.uint32)          # many ties
+            payload = g.integers(0, 1 << 63, size=n, dtype=np.uint64)
+            kb = s.alloc_sort_buffer("u32", n)
+            kb.copy_from_slice(keys)
+            pb = s.alloc_sort_buffer("u64", n)
+            pb.copy_from_slice(payload)
+            ib = s.alloc_sort_buffer("u32", n)
+            ob = s.alloc_sort_buffer("u64", n)
+            s.encode(OP_ARGSORT, "u32", kb.device_ptr(), ib.device_ptr(), n, stream=hip_stream)
+            ptr, _, cap = ib.into_raw_parts()            # the index buffer changes owner
+            ib.free()                                    # no longer owns it: frees nothing
+            idx = SortBuffer.from_raw_parts(s, "u32", ptr, n, cap)
+            ga.encode_gather(pb.device_ptr(), idx.device_ptr(), ob.device_ptr(), n, True, n, stream=hip_stream)
+            ga.synchronize()                             # the one wait: the stream orders sort then gather
+            s.synchronize()
+            ob.set_len(n)
+            order = oracle.argsort("u32", keys)
+            assert np.array_equal(idx.as_slice(), order), f"argsort n={n}"
+            assert np.array_equal(ob.as_slice(), payload[order]), f"gathered column n={n}"
+            for b in (kb, pb, idx, ob):
+                b.free()
+    finally:
+        ga.close()
+        s.close()
+
+
+def gpu_search_keys(n, seed):
+    """gpu-search's composite result keys (content.rs:849-885): (file_index << 32)
+    | byte_offset for matches in search order - files of very different match
+    counts (Zipf), offsets within each file, emitted by parallel workers in
+    interleaved chunks, with repeated (file, offset) pairs."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    files = np.minimum(g.zipf(1.3, size=n) - 1, 199_999).astype(np.uint64)
+    offsets = g.integers(0, 1 << 24, size=n, dtype=np.uint64)
+    offsets[g.random(n) < 0.05] = 4096                  # a common offset: repeated (file, offset) pairs
+    chunks = g.permutation((n + 4095) // 4096)           # interleaved worker output
+    order = np.concatenate([np.arange(c * 4096, min((c + 1) * 4096, n)) for c in chunks])
+    return ((files << np.uint64(32)) | offsets)[order].astype(np.uint64), files[order], offsets[order]
+
+
+@pytest.mark.parametrize("n", [1_048_576, 16_777_216])
+def test_gpu_search_composite_key_argsort(sorter, n):
+    """The gpu-search caller's u64 argsort: equal to the oracle's stable
+    argsort and to the caller's own CPU fallback order (a stable sort by
+    file_index, then byte_offset, content.rs:876-881), computed here by numpy's
+    stable lexsort of the two columns."""
+    keys, files, offsets = gpu_search_keys(n, seed=70 + (n >> 20))
+    got = sorter.argsort_u64(keys)
+    assert np.array_equal(got, oracle.argsort("u64", keys))
+    assert np.array_equal(got, np.lexsort((offsets, files)).astype(np.uint32))
+    passes, mask = sorter.last_pass_info()
+    assert mask & 0xF0 and passes < 8       # the file index's high bytes are constant: skipped
