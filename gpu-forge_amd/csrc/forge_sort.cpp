@@ -40,9 +40,10 @@ struct ProfEntry {
 const char* const kKernelNames[] = {
     "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
+    "fs_scratch_address",
 };
 enum {
-    K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_COUNT
+    K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_COUNT
 };
 
 }  // namespace
@@ -70,6 +71,10 @@ struct fs_sorter {
     // A sort was enqueued on a capturing stream: a HIP graph may hold the
     // addresses of the scratch buffers, so they must not be reallocated.
     bool captured = false;
+
+    // Device address of the code object's static scratch array (fs_encode_no_alloc),
+    // reported by fs_scratch_address once, when the module is loaded.
+    void* na_scratch = nullptr;
 
     // Test options (fs_sorter_set_test_option); defaults give the product layout.
     bool force_wide = false;             // 64-bit look-back entries for any n
@@ -212,15 +217,16 @@ static void recycle_profile(fs_sorter* s) {
 }
 
 static fs_status launch(fs_sorter* s, int k, unsigned grid, unsigned block, void** args,
-                        hipStream_t st) {
+                        hipStream_t st, bool no_events = false) {
     ProfEntry pe{kKernelNames[k], nullptr, nullptr};
-    if (s->profiling) {
+    const bool profiling = s->profiling && !no_events;
+    if (profiling) {
         pe.start = take_event(s);
         pe.stop = take_event(s);
         if (pe.start) HIP_TRY(s, hipEventRecord(pe.start, st));
     }
     HIP_TRY(s, hipModuleLaunchKernel(s->fn[k], grid, 1, 1, block, 1, 1, 0, st, args, nullptr));
-    if (s->profiling) {
+    if (profiling) {
         if (pe.stop) HIP_TRY(s, hipEventRecord(pe.stop, st));
         s->prof.push_back(pe);
     }
@@ -233,6 +239,7 @@ static fs_status launch(fs_sorter* s, int k, unsigned grid, unsigned block, void
 static void reset_device_tables(fs_sorter* s) {
     (void)hipMemset(s->hist, 0, (size_t)FS_MAX_DIGITS * FS_RADIX * 4);
     (void)hipMemset(s->plan, 0, FS_PLAN_WORDS * sizeof(uint32_t));
+    if (s->na_scratch) (void)hipMemset(s->na_scratch, 0, FS_NA_ZERO_BYTES);
     (void)hipDeviceSynchronize();
 }
 
@@ -288,8 +295,31 @@ static fs_status reserve(fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
     return ensure(s, s->lb1, lb_bytes);
 }
 
+// Device addresses of the scratch a sort uses: the sorter's own grow-only
+// buffers, or the static array of fs_encode_no_alloc.
+struct ScratchSet {
+    uint64_t s1k, s2k, s1v, s2v, lb0, lb1, hist, binbase, plan;
+};
+
+static ScratchSet sorter_scratch(const fs_sorter* s) {
+    return ScratchSet{(uint64_t)(uintptr_t)s->s1k.p, (uint64_t)(uintptr_t)s->s2k.p,
+                      (uint64_t)(uintptr_t)s->s1v.p, (uint64_t)(uintptr_t)s->s2v.p,
+                      (uint64_t)(uintptr_t)s->lb0.p, (uint64_t)(uintptr_t)s->lb1.p,
+                      (uint64_t)(uintptr_t)s->hist, (uint64_t)(uintptr_t)s->binbase,
+                      (uint64_t)(uintptr_t)s->plan};
+}
+
+static ScratchSet static_scratch(const fs_sorter* s) {
+    const uint64_t p = (uint64_t)(uintptr_t)s->na_scratch;
+    return ScratchSet{p + FS_NA_OFF_S1K, p + FS_NA_OFF_S2K, p + FS_NA_OFF_S1V, p + FS_NA_OFF_S2V,
+                      p + FS_NA_OFF_LB0, p + FS_NA_OFF_LB1, p + FS_NA_OFF_HIST, p + FS_NA_OFF_BINBASE,
+                      p + FS_NA_OFF_PLAN};
+}
+
+// no_alloc: the sort runs on the static scratch (fs_encode_no_alloc): nothing
+// is allocated, the scratch is not grown and no profiling events are created.
 static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint32_t* vals,
-                         uint64_t n, hipStream_t st) {
+                         uint64_t n, hipStream_t st, bool no_alloc = false) {
     if (!valid_type(t)) return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown key type %d", (int)t);
     if (op != FS_OP_SORT && op != FS_OP_ARGSORT && op != FS_OP_PAIRS)
         return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown op %d", (int)op);
@@ -303,7 +333,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         if (n == 1 && op == FS_OP_ARGSORT) {
             uint64_t one = 1;
             void* args[] = {&vals, &one};
-            fs_status r = launch(s, K_IOTA, 1, 64, args, st);
+            fs_status r = launch(s, K_IOTA, 1, 64, args, st, no_alloc);
             if (r != FS_OK) return r;
         }
         return FS_OK;
@@ -315,9 +345,20 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     const int var = variant_of(op, t);
     const uint32_t tile = s->tile[var];
     const uint32_t num_tiles = (uint32_t)((n + tile - 1) / tile);
-    const bool wide = wide_lookback(s, n);
+    // the static scratch holds narrow look-back entries (n < 2^30 there)
+    const bool wide = !no_alloc && wide_lookback(s, n);
     fs_status r;
-    if ((r = reserve(s, op, t, n)) != FS_OK) return r;
+    if (no_alloc) {
+        if (n > FS_NA_MAX_KEYS)
+            return set_err(s, FS_ERR_INVALID_ARGUMENT,
+                           "n = %llu exceeds the %u keys the no-allocation scratch holds (use fs_encode)",
+                           (unsigned long long)n, (unsigned)FS_NA_MAX_KEYS);
+        if (num_tiles > FS_NA_MAX_TILES)      // every variant's tile is at least FS_NA_MIN_TILE keys
+            return set_err(s, FS_ERR_INVALID_ARGUMENT, "tile geometry exceeds the no-allocation scratch layout");
+    } else if ((r = reserve(s, op, t, n)) != FS_OK) {
+        return r;
+    }
+    const ScratchSet sc = no_alloc ? static_scratch(s) : sorter_scratch(s);
 
     FsArgs a;
     memset(&a, 0, sizeof a);
@@ -343,15 +384,15 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     if (up_blocks == 0) up_blocks = 1;
     a.keys = (uint64_t)(uintptr_t)keys;
     a.vals = (uint64_t)(uintptr_t)vals;
-    a.s1k = (uint64_t)(uintptr_t)s->s1k.p;
-    a.s2k = (uint64_t)(uintptr_t)s->s2k.p;
-    a.s1v = (uint64_t)(uintptr_t)s->s1v.p;
-    a.s2v = (uint64_t)(uintptr_t)s->s2v.p;
-    a.hist = (uint64_t)(uintptr_t)s->hist;
-    a.binbase = (uint64_t)(uintptr_t)s->binbase;
-    a.lookback0 = (uint64_t)(uintptr_t)s->lb0.p;
-    a.lookback1 = (uint64_t)(uintptr_t)s->lb1.p;
-    a.plan = (uint64_t)(uintptr_t)s->plan;
+    a.s1k = sc.s1k;
+    a.s2k = sc.s2k;
+    a.s1v = sc.s1v;
+    a.s2v = sc.s2v;
+    a.hist = sc.hist;
+    a.binbase = sc.binbase;
+    a.lookback0 = sc.lb0;
+    a.lookback1 = sc.lb1;
+    a.plan = sc.plan;
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 #ifdef FS_FAULT_INJECTION
@@ -361,7 +402,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
 
     const unsigned up_grid = (unsigned)up_blocks;
     void* args1[] = {&a};
-    if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st)) != FS_OK) return r;
+    if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK) return r;
     const int os = K_OS32 + var;   // kernel order matches FS_VAR_*
     for (uint32_t d = 0; d < a.digits; ++d) {
         uint32_t digit = d;
@@ -373,7 +414,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
 #ifdef FS_FAULT_INJECTION
         if (s->fault == FS_FAULT_EXTRA_BLOCK && d == 0) grid += 1u;
 #endif
-        if ((r = launch(s, k, grid, s->block[var], args2, st)) != FS_OK) return r;
+        if ((r = launch(s, k, grid, s->block[var], args2, st, no_alloc)) != FS_OK) return r;
     }
     s->last_stream = st;
     s->pending = true;
@@ -487,6 +528,24 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
         hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
         return create_failed(s, FS_ERR_OUT_OF_MEMORY, "device tables of the sorter");
     *s->status = 0;
+    {
+        // The static scratch of fs_encode_no_alloc: its address in this
+        // module, from the kernel (the module API has no symbol for a
+        // file-scope static); its tables must start at zero.
+        uint64_t* out = (uint64_t*)s->stats;
+        void* args[] = {&out};
+        uint64_t got[2] = {0, 0};
+        if (hipModuleLaunchKernel(s->fn[K_SCRATCH_ADDR], 1, 1, 1, 64, 1, 1, 0, s->stream, args, nullptr) != hipSuccess ||
+            hipStreamSynchronize(s->stream) != hipSuccess ||
+            hipMemcpy(got, s->stats, sizeof got, hipMemcpyDeviceToHost) != hipSuccess)
+            return create_failed(s, FS_ERR_GPU_EXECUTION, "querying the no-allocation scratch address");
+        if (got[0] == 0 || got[0] % 256 != 0 || got[1] != FS_NA_SCRATCH_BYTES)
+            return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object's no-allocation scratch has an unexpected "
+                                 "address or size (rebuild the code object and the library together)");
+        s->na_scratch = (void*)(uintptr_t)got[0];
+        if (hipMemset(s->na_scratch, 0, FS_NA_ZERO_BYTES) != hipSuccess)
+            return create_failed(s, FS_ERR_GPU_EXECUTION, "clearing the no-allocation scratch tables");
+    }
     // The histogram table and the upsweep's ticket must start at zero; the
     // upsweep's last block re-zeroes both after every sort.
     if (hipMemset(s->hist, 0, tab) != hipSuccess ||
@@ -610,6 +669,26 @@ fs_status fs_encode(fs_sorter* s, fs_op op, fs_key_type type, void* device_keys,
         if (r != FS_OK) return r;
     }
     return enqueue(s, op, type, device_keys, op == FS_OP_SORT ? nullptr : device_values, n, st);
+}
+
+fs_status fs_encode_no_alloc(fs_sorter* s, fs_op op, fs_key_type type, void* device_keys,
+                             uint32_t* device_values, uint64_t n, void* hip_stream) {
+    if (!s) return FS_ERR_INVALID_ARGUMENT;
+    HIP_TRY(s, hipSetDevice(s->device));
+    hipStream_t st = hip_stream ? (hipStream_t)hip_stream : s->stream;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
+        (void)hipGetLastError();
+        cap = hipStreamCaptureStatusNone;
+    }
+    // The static scratch is shared by every call through this sorter: a sort
+    // on another stream must be done before this one starts (not waited for
+    // while capturing, where the caller orders the work).
+    if (cap != hipStreamCaptureStatusActive && s->pending && s->last_stream != st) {
+        fs_status r = drain(s);
+        if (r != FS_OK) return r;
+    }
+    return enqueue(s, op, type, device_keys, op == FS_OP_SORT ? nullptr : device_values, n, st, true);
 }
 
 fs_status fs_reserve(fs_sorter* s, fs_op op, fs_key_type type, uint64_t n) {

@@ -179,6 +179,35 @@
 #define FS_FAULT_EXTRA_BLOCK 3u    // first digit pass launched with one block too many -> BAD_TILE
 #define FS_FAULT_STALL_TILE 4u     // tile 1 of the first pass never publishes -> LOOKBACK_TIMEOUT
 
+// Scratch of the entry point that allocates nothing (fs_encode_no_alloc): a
+// file-scope static device array of FS_NA_SCRATCH_BYTES in the code object,
+// laid out as the histogram, bin-base and schedule tables, the two look-back
+// arrays and the key/value ping-pong buffers for sorts of up to
+// FS_NA_MAX_KEYS keys of any type and op (64-bit keys with values: the
+// largest).  Offsets in bytes, each 256-byte aligned.
+#define FS_NA_MAX_KEYS (1u << 20)
+#define FS_NA_ALIGN(x) ((((x) + 255ull) / 256ull) * 256ull)
+#define FS_MIN2(a, b) ((a) < (b) ? (a) : (b))
+#define FS_NA_MIN_TILE FS_MIN2(FS_MIN2(FS_K32_BLOCK * FS_K32_ITEMS, FS_K32V_BLOCK * FS_K32V_ITEMS), \
+                               FS_MIN2(FS_K64_BLOCK * FS_K64_ITEMS, FS_K64V_BLOCK * FS_K64V_ITEMS))
+#define FS_NA_MAX_TILES ((FS_NA_MAX_KEYS + FS_NA_MIN_TILE - 1) / FS_NA_MIN_TILE)
+#define FS_NA_TABLE_BYTES FS_NA_ALIGN((unsigned long long)FS_MAX_DIGITS * FS_RADIX * 4)
+#define FS_NA_LB_BYTES FS_NA_ALIGN((unsigned long long)FS_NA_MAX_TILES * FS_RADIX * 4 + \
+                                   (unsigned long long)((FS_NA_MAX_TILES + FS_LB_GROUP - 1) / FS_LB_GROUP) * FS_RADIX * 4)
+#define FS_NA_OFF_HIST 0ull
+#define FS_NA_OFF_BINBASE (FS_NA_OFF_HIST + FS_NA_TABLE_BYTES)
+#define FS_NA_OFF_PLAN (FS_NA_OFF_BINBASE + FS_NA_TABLE_BYTES)
+#define FS_NA_OFF_LB0 (FS_NA_OFF_PLAN + FS_NA_ALIGN(FS_PLAN_WORDS * 4))
+#define FS_NA_OFF_LB1 (FS_NA_OFF_LB0 + FS_NA_LB_BYTES)
+#define FS_NA_OFF_S1K (FS_NA_OFF_LB1 + FS_NA_LB_BYTES)
+#define FS_NA_OFF_S2K (FS_NA_OFF_S1K + (unsigned long long)FS_NA_MAX_KEYS * 8)
+#define FS_NA_OFF_S1V (FS_NA_OFF_S2K + (unsigned long long)FS_NA_MAX_KEYS * 8)
+#define FS_NA_OFF_S2V (FS_NA_OFF_S1V + (unsigned long long)FS_NA_MAX_KEYS * 4)
+#define FS_NA_SCRATCH_BYTES (FS_NA_OFF_S2V + (unsigned long long)FS_NA_MAX_KEYS * 4)
+// bytes that must be zero before the first sort (histogram, and the
+// schedule with the upsweep's ticket); every sort leaves them zero again
+#define FS_NA_ZERO_BYTES FS_NA_OFF_LB0
+
 // Kernel argument block, passed by value to every kernel.
 typedef struct FsArgs {
     uint64_t n;                 // number of keys (2 <= n < 2^32)

@@ -33,6 +33,7 @@ NP_DTYPES = {"u32": np.uint32, "i32": np.int32, "f32": np.float32,
              "u64": np.uint64, "i64": np.int64, "f64": np.float64}
 KEY_SIZE = {"u32": 4, "i32": 4, "f32": 4, "u64": 8, "i64": 8, "f64": 8}   # SortKey::KEY_SIZE
 OP_SORT, OP_ARGSORT, OP_PAIRS = 0, 1, 2
+NO_ALLOC_MAX_KEYS = 1 << 20          # FS_NO_ALLOC_MAX_KEYS
 # fs_test_option and the FS_FAULT_* codes (include/forge_sort.h, csrc/fs_params.h)
 TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT = 0, 1, 2
 FAULT_NONE, FAULT_BAD_DIGITS, FAULT_BAD_BUFFER, FAULT_EXTRA_BLOCK, FAULT_STALL_TILE = 0, 1, 2, 3, 4
@@ -124,6 +125,7 @@ def _load():
         "fs_argsort_buffer": ([vp, i, vp, u64, vp], i),
         "fs_sort_pairs_buffer": ([vp, i, vp, vp, u64], i),
         "fs_encode": ([vp, i, i, vp, vp, u64, vp], i),
+        "fs_encode_no_alloc": ([vp, i, i, vp, vp, u64, vp], i),
         "fs_reserve": ([vp, i, i, u64], i),
         "fs_allow_scratch_growth": ([vp], i),
         "fs_sorter_set_test_option": ([vp, i, u64], i),
@@ -355,6 +357,13 @@ class GpuSorter:
         self._check(_load().fs_encode(self._h, op, KEY_TYPES[kind], ctypes.c_void_p(keys_ptr),
                                       ctypes.c_void_p(values_ptr or 0), n,
                                       ctypes.c_void_p(stream or 0)))
+
+    def encode_no_alloc(self, op, kind, keys_ptr, values_ptr, n, stream=None):
+        """encode() on the code object's static scratch: allocates nothing;
+        n <= NO_ALLOC_MAX_KEYS; calls through one sorter must not overlap."""
+        self._check(_load().fs_encode_no_alloc(self._h, op, KEY_TYPES[kind], ctypes.c_void_p(keys_ptr),
+                                               ctypes.c_void_p(values_ptr or 0), n,
+                                               ctypes.c_void_p(stream or 0)))
 
     def synchronize(self):
         self._check(_load().fs_synchronize(self._h))

@@ -151,6 +151,24 @@ fs_status fs_sort_pairs_buffer(fs_sorter *s, fs_key_type type, void *device_keys
 fs_status fs_encode(fs_sorter *s, fs_op op, fs_key_type type, void *device_keys,
                     uint32_t *device_values, uint64_t n, void *hip_stream);
 
+/* fs_encode for callers that cannot allocate: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  No counterpart in the
+ * reference.  Same arguments and results as fs_encode, but every scratch
+ * buffer of the sort (histogram, bin-base and schedule tables, look-back
+ * arrays, key and value ping-pong buffers) lives in a static array of the
+ * loaded code object (FS_NO_ALLOC_SCRATCH_BYTES, held by each sorter until
+ * fs_sorter_free), so the call allocates and frees nothing and never grows
+ * anything: n is limited to FS_NO_ALLOC_MAX_KEYS keys of any type and op
+ * (FS_ERR_INVALID_ARGUMENT beyond).  Every call through one sorter uses the
+ * same array and finds the last call's contents in it (the kernels leave the
+ * tables cleared for the next sort): calls through one sorter that overlap on
+ * the device race, so issue them on one stream or order them.  fs_encode's
+ * scratch is separate. */
+#define FS_NO_ALLOC_MAX_KEYS 1048576u
+#define FS_NO_ALLOC_SCRATCH_BYTES 25481472u   /* 24.3 MiB with the gfx950 tile geometry */
+fs_status fs_encode_no_alloc(fs_sorter *s, fs_op op, fs_key_type type, void *device_keys,
+                             uint32_t *device_values, uint64_t n, void *hip_stream);
+
 /* Grow the sorter's scratch for sorts of up to n keys of `type` with `op`
  * (the grow-only ensure_buffers*, lib.rs:1120-1289, done ahead of time), e.g.
  * before capturing a sort into a HIP graph.  Synchronous. */

@@ -19,6 +19,7 @@
 #define __launch_bounds__(...)
 #define __constant__
 #define __shared__ static thread_local
+#define __align__(n) __attribute__((aligned(n)))
 
 struct uint4 { uint32_t x, y, z, w; };
 struct emu_dim3 { uint32_t x, y, z; };

@@ -311,6 +311,7 @@ void fs_onesweep_k64_v(FsArgs, uint32_t);
 void fs_onesweep_any_k32(FsArgs, uint32_t);
 void fs_onesweep_any_k64(FsArgs, uint32_t);
 void fs_iota(uint32_t*, uint64_t);
+void fs_scratch_address(uint64_t*);
 void fs_gather_elems(uint64_t, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint64_t);
 extern uint32_t fs_kernel_tile_keys[4];
 extern uint32_t fs_kernel_block_threads[4];
@@ -333,6 +334,7 @@ static emu_function g_funcs[] = {
     {"fs_onesweep_any_k32", [](void** p) { fs_onesweep_any_k32(A0, D1); }},
     {"fs_onesweep_any_k64", [](void** p) { fs_onesweep_any_k64(A0, D1); }},
     {"fs_iota", [](void** p) { fs_iota(*(uint32_t**)p[0], *(uint64_t*)p[1]); }},
+    {"fs_scratch_address", [](void** p) { fs_scratch_address(*(uint64_t**)p[0]); }},
     {"fs_gather_elems", [](void** p) {
          fs_gather_elems(*(uint64_t*)p[0], *(uint64_t*)p[1], *(uint64_t*)p[2], *(uint64_t*)p[3],
                          *(uint64_t*)p[4], *(uint32_t*)p[5], *(uint64_t*)p[6]);

@@ -181,7 +181,40 @@ def check_capture(sorter, kind, n, seed):
     return ok
 
 
+def check_no_alloc(sorter, kind, n, dist, seed):
+    """fs_encode_no_alloc (static scratch) against fs_encode for every op,
+    then the same with a smaller input (which finds the first call's contents
+    in the static scratch)."""
+    ok = True
+    for m in (n, n // 3 + 1):
+        keys = keys_for(kind, m, dist, seed + m)
+        vals = np.arange(m, dtype=np.uint32)[::-1].copy()
+        for op in (forge_sort.OP_SORT, forge_sort.OP_ARGSORT, forge_sort.OP_PAIRS):
+            outs = []
+            for no_alloc in (False, True):
+                kb = sorter.alloc_sort_buffer(kind, m)
+                kb.copy_from_slice(keys)
+                vb = sorter.alloc_sort_buffer("u32", m)
+                if op == forge_sort.OP_PAIRS:
+                    vb.copy_from_slice(vals)
+                enc = sorter.encode_no_alloc if no_alloc else sorter.encode
+                enc(op, kind, kb.device_ptr(), vb.device_ptr(), m)
+                sorter.synchronize()
+                vb.set_len(m)
+                outs.append((kb.as_slice().view(BITS[kind]), vb.as_slice()))
+                kb.free()
+                vb.free()
+            ok &= bool(np.array_equal(outs[0][0], outs[1][0]))
+            if op != forge_sort.OP_SORT:
+                ok &= bool(np.array_equal(outs[0][1], outs[1][1]))
+    return ok
+
+
 def check(sorter, op, kind, n, dist, seed):
+    if op == "noalloc":
+        ok = check_no_alloc(sorter, kind, n, dist, seed)
+        print(f"{'PASS' if ok else 'FAIL'} {op} {kind} n={n}", flush=True)
+        return ok
     if op in FAULTS or op in ("hold", "capture"):
         if op == "capture":
             ok = check_capture(sorter, kind, n, seed)

@@ -57,3 +57,20 @@ def test_no_device_is_reported_not_raised_as_crash():
         return
     s.close()
     pytest.skip("a GPU is present")
+
+
+def test_no_alloc_limits_match_the_scratch_layout(tmp_path):
+    """The header's FS_NO_ALLOC_* constants equal the static scratch layout the
+    gfx950 build compiles (fs_params.h with its default tile geometry)."""
+    import subprocess
+    src = tmp_path / "na.c"
+    src.write_text(
+        '#include "fs_params.h"\n#include "forge_sort.h"\n'
+        "_Static_assert(FS_NA_SCRATCH_BYTES == FS_NO_ALLOC_SCRATCH_BYTES, \"scratch bytes\");\n"
+        "_Static_assert(FS_NA_MAX_KEYS == FS_NO_ALLOC_MAX_KEYS, \"max keys\");\n"
+        "_Static_assert(FS_NA_OFF_S1K % 256 == 0 && FS_NA_OFF_LB0 % 256 == 0, \"aligned\");\n"
+        "int main(void) { return 0; }\n")
+    r = subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "gpu-forge_amd", "csrc"),
+                        "-I", os.path.join(ROOT, "include"), str(src), "-o", str(tmp_path / "na")],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

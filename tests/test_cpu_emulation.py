@@ -147,6 +147,12 @@ def test_emulated_held_xcd_queue(emulator):
     run_cases("faults", ["hold:u32:40000:uniform:1"], env={"EMU_CUS": "8", "EMU_HOLD_QUEUE": "3:1000"})
 
 
+def test_emulated_no_alloc_entry_point(emulator):
+    """fs_encode_no_alloc (static scratch, no allocation) gives fs_encode's
+    results for every op, on two calls in a row, the second smaller."""
+    run_cases("small", ["noalloc:u32:9000:uniform:1", "noalloc:f64:5000:few:2", "noalloc:i32:4099:zipf:3"])
+
+
 def test_emulated_capture_rules(emulator):
     """A sort enqueued on a capturing stream fits the reserved scratch or is
     refused; after a capture, growth is refused until fs_allow_scratch_growth."""
