@@ -281,6 +281,7 @@ def main():
     prof = sorter.profile()
     sorter.set_profiling(False)
     _, digit_mask = sorter.last_pass_info()      # digits whose pass ran (same input every step)
+    first_kind = sorter.first_pass()             # how each sort began (same input every step)
     log(f"bench: timed {K} sorts in {t1 - t0:.4f} s")
 
     # the last output: sorted, same multiset, stable for argsort and pairs
@@ -316,10 +317,13 @@ def main():
     for name, ms in prof:
         by_kernel.setdefault(name, []).append(ms)
     # every sort launches one digit pass per digit position, in digit order; a
-    # constant digit's launch exits at once and is not averaged
+    # constant digit's launch exits at once and is not averaged.  Keys-only
+    # sorts launch digit 0 on the any-order kernel (or sort it in the fused
+    # first pass), so the stable kernel runs digits 1.. there.
     digits = ksize                                 # 8-bit digits: one per key byte
+    pass_digits = list(range(1 if op == OP_SORT else 0, digits))
     passes = by_kernel.get(pass_kernel, [])
-    active = [ms for i, ms in enumerate(passes) if digit_mask >> (i % digits) & 1]
+    active = [ms for i, ms in enumerate(passes) if digit_mask >> pass_digits[i % len(pass_digits)] & 1]
     pass_ms = float(np.mean(active)) if active else float("nan")
     achieved = pass_bytes * n / (pass_ms / 1e3) / 1e9
     kernel_sum_ms = sum(ms for _, ms in prof) / K
@@ -334,6 +338,15 @@ def main():
     }
     kernels = {k: {"avg_ms": round(float(np.mean(v)), 4), "launches": len(v)}
                for k, v in sorted(by_kernel.items())}
+    # the first kernel of each sort: the fused first pass (one read and one
+    # write of every key, the other digits counted on the way) or the histogram
+    # read (one read of every key)
+    first_kernel = ("fs_first_" if first_kind else "fs_upsweep_") + ("k64" if ksize == 8 else "k32")
+    first_ms = float(np.mean(by_kernel[first_kernel])) if by_kernel.get(first_kernel) else float("nan")
+    first_bytes = (2 if first_kind else 1) * ksize * n
+    first_pass = {"kind": ["histogram read", "fused first pass", "fused first pass, region overflow"][first_kind],
+                  "kernel": first_kernel, "avg_ms": round(first_ms, 4), "bytes_algorithmic": first_bytes,
+                  "achieved_GBps": round(first_bytes / (first_ms / 1e3) / 1e9, 1)}
     sort_frac = sort_bytes * n / (ms_per_step / 1e3) / (HBM_PEAK_GBS * 1e9)
 
     # The slice API (sort_u32 on a host array: copy in, sort, copy out), reported
@@ -383,6 +396,7 @@ def main():
                           "achieved_GBps": round(sort_frac * HBM_PEAK_GBS, 1)},
         "oracle_match": cpu["oracle_match"] if cpu else None,
         "exact_match": cpu["oracle_match"] if cpu else exact,
+        "first_pass": first_pass,
         "kernels": kernels, "kernel_ms_per_step": round(kernel_sum_ms, 4),
         "slice_api": slice_api,
         "cpu_baseline": cpu,

@@ -40,10 +40,11 @@ struct ProfEntry {
 const char* const kKernelNames[] = {
     "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
-    "fs_scratch_address",
+    "fs_scratch_address", "fs_first_k32", "fs_first_k64",
 };
 enum {
-    K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_COUNT
+    K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
+    K_COUNT
 };
 
 }  // namespace
@@ -58,9 +59,11 @@ struct fs_sorter {
     uint32_t block[4] = {};         // threads per block of each variant
     int num_cus = 256;
 
-    DevBuf s1k, s2k, s1v, s2v, lb0, lb1, iok, iov;
-    uint32_t* hist = nullptr;       // [8][256], zero between sorts
+    DevBuf s1k, s2k, s1v, s2v, lb0, lb1, iok, iov, tilemap;
+    uint32_t* hist = nullptr;       // [FS_HIST_SLOTS][8][256], zero between sorts
     uint32_t* binbase = nullptr;    // [8][256]
+    uint32_t* cursors = nullptr;    // [FS_REGIONS] region cursors of the fused pass, zero between sorts
+    uint32_t* rstart = nullptr;     // [FS_REGIONS + 1] region starts
     uint32_t* plan = nullptr;       // u32[FS_PLAN_WORDS] device-side schedule
     uint32_t* status = nullptr;     // pinned host word written by kernels on device errors
     unsigned long long* stats = nullptr;   // device u64[FS_STAT_COUNT]
@@ -78,6 +81,11 @@ struct fs_sorter {
 
     // Test options (fs_sorter_set_test_option); defaults give the product layout.
     bool force_wide = false;             // 64-bit look-back entries for any n
+    uint32_t fused_mode = 0;             // FS_TEST_FUSED: 0 by size, 1 never, 2 always
+    // the last sort's schedule (the sorter's, or the static scratch's) and
+    // whether it began with the fused first pass
+    uint32_t* last_plan = nullptr;
+    bool last_fused = false;
     uint32_t up_blocks_per_cu = 0;       // upsweep blocks per CU (0: by key width)
     uint32_t fault = FS_FAULT_NONE;      // injected fault (FS_FAULT_INJECTION builds only)
 
@@ -237,8 +245,9 @@ static fs_status launch(fs_sorter* s, int k, unsigned grid, unsigned block, void
 // ticket) are cleared, so the next sort starts from the state every sort
 // leaves behind.  The device is idle here (the caller has synchronised).
 static void reset_device_tables(fs_sorter* s) {
-    (void)hipMemset(s->hist, 0, (size_t)FS_MAX_DIGITS * FS_RADIX * 4);
+    (void)hipMemset(s->hist, 0, (size_t)FS_HIST_WORDS * 4);
     (void)hipMemset(s->plan, 0, FS_PLAN_WORDS * sizeof(uint32_t));
+    (void)hipMemset(s->cursors, 0, FS_REGIONS * sizeof(uint32_t));
     if (s->na_scratch) (void)hipMemset(s->na_scratch, 0, FS_NA_ZERO_BYTES);
     (void)hipDeviceSynchronize();
 }
@@ -273,6 +282,27 @@ static int variant_of(fs_op op, fs_key_type t) {
 // than 30 bits, or when a test forces that layout.
 static bool wide_lookback(const fs_sorter* s, uint64_t n) { return n >= FS_LB_WIDE_KEYS || s->force_wide; }
 
+// Keys per region of the fused first pass (fs_params.h): tile t writes the
+// regions of group (t / FS_XCD_TILES) % FS_SUBS, so a region receives about
+// 1/FS_RADIX of its group's keys; the cap is 1.5x that share of the largest
+// group, plus a margin, so that uniform keys never overflow a region.
+static uint64_t region_cap(uint64_t n, uint32_t tile) {
+    const uint64_t tiles = (n + tile - 1) / tile;
+    const uint64_t runs = (tiles + FS_XCD_TILES - 1) / FS_XCD_TILES;    // runs of FS_XCD_TILES tiles
+    const uint64_t most = (runs + FS_SUBS - 1) / FS_SUBS;              // group 0 has the most runs
+    uint64_t keys = most * FS_XCD_TILES * tile;
+    if (keys > n) keys = n;
+    return (3 * keys) / (2 * FS_RADIX) + 64;
+}
+
+// Keys-only sorts of 32-bit keys start with the fused first pass (no
+// histogram read); S1 then holds FS_REGIONS regions, which must stay below
+// 2^32 keys (n <= 2^31 keeps them below 1.5 n + 2^17).
+static bool fused_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
+    if (op != FS_OP_SORT || key64(t) || n > (1ull << 31) || s->fused_mode == 1u) return false;
+    return s->fused_mode == 2u || n >= FS_FUSED_MIN_KEYS;
+}
+
 // Grows the scratch a sort of n keys needs (grow-only, like ensure_buffers*,
 // lib.rs:1120-1289): ping-pong buffers for keys (and values), and two
 // look-back arrays of tile entries followed by one 32-bit group entry per
@@ -283,8 +313,10 @@ static fs_status reserve(fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
     const uint32_t tile = s->tile[variant_of(op, t)];
     const uint64_t num_tiles = (n + tile - 1) / tile;
     fs_status r;
-    if ((r = ensure(s, s->s1k, n * kb)) != FS_OK) return r;
+    const bool fused = fused_path(s, op, t, n);
+    if ((r = ensure(s, s->s1k, (fused ? FS_REGIONS * region_cap(n, tile) : n) * kb)) != FS_OK) return r;
     if ((r = ensure(s, s->s2k, n * kb)) != FS_OK) return r;
+    if (fused && (r = ensure(s, s->tilemap, num_tiles * FS_TILE_DESC_WORDS * 4)) != FS_OK) return r;
     if (op != FS_OP_SORT) {
         if ((r = ensure(s, s->s1v, n * 4)) != FS_OK) return r;
         if (op == FS_OP_PAIRS && (r = ensure(s, s->s2v, n * 4)) != FS_OK) return r;
@@ -298,7 +330,7 @@ static fs_status reserve(fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
 // Device addresses of the scratch a sort uses: the sorter's own grow-only
 // buffers, or the static array of fs_encode_no_alloc.
 struct ScratchSet {
-    uint64_t s1k, s2k, s1v, s2v, lb0, lb1, hist, binbase, plan;
+    uint64_t s1k, s2k, s1v, s2v, lb0, lb1, hist, binbase, plan, cursors, rstart, tilemap;
 };
 
 static ScratchSet sorter_scratch(const fs_sorter* s) {
@@ -306,14 +338,15 @@ static ScratchSet sorter_scratch(const fs_sorter* s) {
                       (uint64_t)(uintptr_t)s->s1v.p, (uint64_t)(uintptr_t)s->s2v.p,
                       (uint64_t)(uintptr_t)s->lb0.p, (uint64_t)(uintptr_t)s->lb1.p,
                       (uint64_t)(uintptr_t)s->hist, (uint64_t)(uintptr_t)s->binbase,
-                      (uint64_t)(uintptr_t)s->plan};
+                      (uint64_t)(uintptr_t)s->plan, (uint64_t)(uintptr_t)s->cursors,
+                      (uint64_t)(uintptr_t)s->rstart, (uint64_t)(uintptr_t)s->tilemap.p};
 }
 
 static ScratchSet static_scratch(const fs_sorter* s) {
     const uint64_t p = (uint64_t)(uintptr_t)s->na_scratch;
     return ScratchSet{p + FS_NA_OFF_S1K, p + FS_NA_OFF_S2K, p + FS_NA_OFF_S1V, p + FS_NA_OFF_S2V,
                       p + FS_NA_OFF_LB0, p + FS_NA_OFF_LB1, p + FS_NA_OFF_HIST, p + FS_NA_OFF_BINBASE,
-                      p + FS_NA_OFF_PLAN};
+                      p + FS_NA_OFF_PLAN, p + FS_NA_OFF_CURSORS, p + FS_NA_OFF_RSTART, p + FS_NA_OFF_TILEMAP};
 }
 
 // no_alloc: the sort runs on the static scratch (fs_encode_no_alloc): nothing
@@ -359,6 +392,10 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         return r;
     }
     const ScratchSet sc = no_alloc ? static_scratch(s) : sorter_scratch(s);
+    // the fused first pass, when its regions fit the scratch (the static
+    // scratch's S1 holds FS_NA_MAX_KEYS 8-byte keys)
+    const bool fused = fused_path(s, op, t, n) &&
+                       (!no_alloc || FS_REGIONS * region_cap(n, tile) * kb <= (uint64_t)FS_NA_MAX_KEYS * 8);
 
     FsArgs a;
     memset(&a, 0, sizeof a);
@@ -393,6 +430,11 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.lookback0 = sc.lb0;
     a.lookback1 = sc.lb1;
     a.plan = sc.plan;
+    a.cursors = sc.cursors;
+    a.rstart = sc.rstart;
+    a.tilemap = sc.tilemap;
+    a.fused = fused ? 1u : 0u;
+    a.region_cap = fused ? (uint32_t)region_cap(n, tile) : 0u;
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 #ifdef FS_FAULT_INJECTION
@@ -400,9 +442,18 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     if (s->fault == FS_FAULT_BAD_DIGITS) a.digits = 5u;
 #endif
 
-    const unsigned up_grid = (unsigned)up_blocks;
     void* args1[] = {&a};
-    if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK) return r;
+    if (fused) {
+        unsigned grid = num_tiles;
+#ifdef FS_FAULT_INJECTION
+        if (s->fault == FS_FAULT_EXTRA_BLOCK) grid += 1u;
+#endif
+        if ((r = launch(s, key64(t) ? K_FIRST64 : K_FIRST32, grid, s->block[var], args1, st, no_alloc)) != FS_OK)
+            return r;
+    } else {
+        const unsigned up_grid = (unsigned)up_blocks;
+        if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK) return r;
+    }
     const int os = K_OS32 + var;   // kernel order matches FS_VAR_*
     for (uint32_t d = 0; d < a.digits; ++d) {
         uint32_t digit = d;
@@ -412,12 +463,14 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         const int k = (d == 0 && op == FS_OP_SORT) ? (key64(t) ? K_ANY64 : K_ANY32) : os;
         unsigned grid = num_tiles;
 #ifdef FS_FAULT_INJECTION
-        if (s->fault == FS_FAULT_EXTRA_BLOCK && d == 0) grid += 1u;
+        if (s->fault == FS_FAULT_EXTRA_BLOCK && d == 0 && !fused) grid += 1u;
 #endif
         if ((r = launch(s, k, grid, s->block[var], args2, st, no_alloc)) != FS_OK) return r;
     }
     s->last_stream = st;
     s->pending = true;
+    s->last_plan = (uint32_t*)(uintptr_t)sc.plan;
+    s->last_fused = fused;
     return FS_OK;
 }
 
@@ -522,7 +575,8 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
                 return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object has an invalid tile geometry");
     }
     const size_t tab = (size_t)FS_MAX_DIGITS * FS_RADIX * 4;
-    if (hipMalloc(&s->hist, tab) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||
+    if (hipMalloc(&s->hist, (size_t)FS_HIST_WORDS * 4) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||
+        hipMalloc(&s->cursors, FS_REGIONS * 4) != hipSuccess || hipMalloc(&s->rstart, (FS_REGIONS + 1) * 4) != hipSuccess ||
         hipMalloc(&s->plan, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc(&s->stats, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
@@ -548,7 +602,8 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
     }
     // The histogram table and the upsweep's ticket must start at zero; the
     // upsweep's last block re-zeroes both after every sort.
-    if (hipMemset(s->hist, 0, tab) != hipSuccess ||
+    if (hipMemset(s->hist, 0, (size_t)FS_HIST_WORDS * 4) != hipSuccess ||
+        hipMemset(s->cursors, 0, FS_REGIONS * 4) != hipSuccess ||
         hipMemset(s->stats, 0, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipMemset(s->plan, 0, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess)
@@ -570,9 +625,11 @@ void fs_sorter_free(fs_sorter* s) {
     if (s->stream || s->own_stream) (void)hipStreamSynchronize(s->stream);
     recycle_profile(s);
     for (hipEvent_t e : s->event_pool) (void)hipEventDestroy(e);
-    DevBuf* bufs[] = {&s->s1k, &s->s2k, &s->s1v, &s->s2v, &s->lb0, &s->lb1, &s->iok, &s->iov};
+    DevBuf* bufs[] = {&s->s1k, &s->s2k, &s->s1v, &s->s2v, &s->lb0, &s->lb1, &s->iok, &s->iov, &s->tilemap};
     for (DevBuf* b : bufs) free_buf(*b);
     if (s->hist) (void)hipFree(s->hist);
+    if (s->cursors) (void)hipFree(s->cursors);
+    if (s->rstart) (void)hipFree(s->rstart);
     if (s->binbase) (void)hipFree(s->binbase);
     if (s->plan) (void)hipFree(s->plan);
     if (s->stats) (void)hipFree(s->stats);
@@ -714,6 +771,10 @@ fs_status fs_sorter_set_test_option(fs_sorter* s, fs_test_option opt, uint64_t v
     if (r != FS_OK) return r;
     switch (opt) {
         case FS_TEST_WIDE_LOOKBACK: s->force_wide = value != 0; return FS_OK;
+        case FS_TEST_FUSED:
+            if (value > 2) return set_err(s, FS_ERR_INVALID_ARGUMENT, "fused mode %llu > 2", (unsigned long long)value);
+            s->fused_mode = (uint32_t)value;
+            return FS_OK;
         case FS_TEST_UPSWEEP_BLOCKS_PER_CU:
             if (value > 64) return set_err(s, FS_ERR_INVALID_ARGUMENT, "upsweep blocks per CU %llu > 64",
                                            (unsigned long long)value);
@@ -862,9 +923,20 @@ fs_status fs_last_pass_info(fs_sorter* s, uint32_t* n_passes, uint32_t* digit_ma
     fs_status r = drain(s);
     if (r != FS_OK) return r;
     uint32_t w[FS_PLAN_WORDS];
-    HIP_TRY(s, hipMemcpy(w, s->plan, sizeof w, hipMemcpyDeviceToHost));
+    HIP_TRY(s, hipMemcpy(w, s->last_plan ? s->last_plan : s->plan, sizeof w, hipMemcpyDeviceToHost));
     if (n_passes) *n_passes = w[FS_PLAN_NPASSES];
-    if (digit_mask) *digit_mask = w[FS_PLAN_MASK];
+    if (digit_mask) *digit_mask = w[FS_PLAN_MASK] & ((1u << FS_MAX_DIGITS) - 1u);
+    return FS_OK;
+}
+
+fs_status fs_sorter_first_pass(fs_sorter* s, uint32_t* kind) {
+    if (!s || !kind) return FS_ERR_INVALID_ARGUMENT;
+    fs_status r = drain(s);
+    if (r != FS_OK) return r;
+    uint32_t mask = 0;
+    HIP_TRY(s, hipMemcpy(&mask, (s->last_plan ? s->last_plan : s->plan) + FS_PLAN_MASK, sizeof mask,
+                         hipMemcpyDeviceToHost));
+    *kind = !s->last_fused ? 0u : (mask & FS_MASK_FUSED) ? 1u : 2u;
     return FS_OK;
 }
 

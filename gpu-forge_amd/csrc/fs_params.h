@@ -126,6 +126,7 @@
 // Per-pass flags in the device-side schedule.
 #define FS_PASS_FIRST 1u   // apply the forward key transform on load; argsort: generate indices
 #define FS_PASS_LAST 2u    // apply the inverse transform on store; argsort: do not store keys
+#define FS_PASS_REGIONED 4u  // the source is the fused first pass's region layout (see below)
 
 // Operation.
 #define FSK_OP_KEYS 0u
@@ -142,6 +143,38 @@
 #define FS_DUTY_NONE 0u
 #define FS_DUTY_COPY 1u    // copy keys (and values) between the buffers named, over the grid
 #define FS_DUTY_IOTA 2u    // argsort with every digit constant: indices = 0..n-1
+#define FS_DUTY_UNREGION 3u  // keys-only, only digit 0 varies: the region layout of S1 -> caller keys,
+                             // with the inverse transform
+
+// Fused first pass of keys-only sorts (fs_first_*).  It reads the caller's
+// keys once, counts the other digits for the later passes (the histogram read
+// a sort otherwise starts with), and scatters the keys by digit 0 into fixed
+// regions of scratch S1: FS_SUBS regions per digit value, region
+// k = digit * FS_SUBS + sub of FsArgs.region_cap keys at S1 + k * region_cap,
+// where sub is the XCD group of the tile.  A tile takes the space of each of
+// its digit runs with one atomic on the region's cursor (an LSD sort's first
+// pass needs no order among equal digits), so the pass has no look-back.  The
+// region start table (virtual position of each region's first key, regions
+// in order) lets the next pass read the keys in digit-0 order.  A region that
+// would overflow drops its runs, and the schedule step falls back to the
+// stable passes over the caller's untouched keys.
+#ifndef FS_SUBS
+#define FS_SUBS 8
+#endif
+#define FS_REGIONS (FS_RADIX * FS_SUBS)
+// Histogram table: FS_HIST_SLOTS copies of [FS_MAX_DIGITS][FS_RADIX]; the
+// fused pass's tiles fold their counts into copy (tile % FS_HIST_SLOTS), so
+// that no counter takes more than num_tiles / FS_HIST_SLOTS atomics.
+#define FS_HIST_SLOTS 16
+// Tile descriptor of the region layout, 4 words {x, y, z, w} per tile of the
+// pass after the fused one.  w = region k0 of the tile's first key, with
+// FS_TILE_MULTI set when the tile covers more than two regions.  Otherwise
+// the S1 index of position p is p + (p < y ? x : z) (y: first position of the
+// second region, or 0xFFFFFFFF); with FS_TILE_MULTI, x is the region of the
+// tile's last key and indices come from the region start table.
+#define FS_TILE_MULTI 0x80000000u
+#define FS_TILE_DESC_WORDS 4
+#define FS_HIST_WORDS (FS_HIST_SLOTS * FS_MAX_DIGITS * FS_RADIX)
 
 // Error bits reported through the host-visible status word.
 #define FS_DEVERR_LOOKBACK_TIMEOUT 1u
@@ -162,6 +195,7 @@
 #define FS_PLAN_PASS_WORDS 2
 #define FS_PLAN_NPASSES (FS_MAX_DIGITS * FS_PLAN_PASS_WORDS)      // passes that run
 #define FS_PLAN_MASK (FS_PLAN_NPASSES + 1)                         // bit j: digit j sorted
+#define FS_MASK_FUSED (1u << 8)     // mask word: digit 0 sorted by the fused first pass's regions
 #define FS_PLAN_TICKET (FS_PLAN_NPASSES + 2)                       // upsweep blocks finished (0 between sorts)
 #define FS_PLAN_WORDS (FS_PLAN_NPASSES + 3)
 
@@ -192,21 +226,25 @@
                                FS_MIN2(FS_K64_BLOCK * FS_K64_ITEMS, FS_K64V_BLOCK * FS_K64V_ITEMS))
 #define FS_NA_MAX_TILES ((FS_NA_MAX_KEYS + FS_NA_MIN_TILE - 1) / FS_NA_MIN_TILE)
 #define FS_NA_TABLE_BYTES FS_NA_ALIGN((unsigned long long)FS_MAX_DIGITS * FS_RADIX * 4)
+#define FS_NA_HIST_BYTES FS_NA_ALIGN((unsigned long long)FS_HIST_WORDS * 4)
 #define FS_NA_LB_BYTES FS_NA_ALIGN((unsigned long long)FS_NA_MAX_TILES * FS_RADIX * 4 + \
                                    (unsigned long long)((FS_NA_MAX_TILES + FS_LB_GROUP - 1) / FS_LB_GROUP) * FS_RADIX * 4)
 #define FS_NA_OFF_HIST 0ull
-#define FS_NA_OFF_BINBASE (FS_NA_OFF_HIST + FS_NA_TABLE_BYTES)
-#define FS_NA_OFF_PLAN (FS_NA_OFF_BINBASE + FS_NA_TABLE_BYTES)
-#define FS_NA_OFF_LB0 (FS_NA_OFF_PLAN + FS_NA_ALIGN(FS_PLAN_WORDS * 4))
+#define FS_NA_OFF_PLAN (FS_NA_OFF_HIST + FS_NA_HIST_BYTES)
+#define FS_NA_OFF_CURSORS (FS_NA_OFF_PLAN + FS_NA_ALIGN(FS_PLAN_WORDS * 4))
+#define FS_NA_OFF_BINBASE (FS_NA_OFF_CURSORS + FS_NA_ALIGN(FS_REGIONS * 4))
+#define FS_NA_OFF_RSTART (FS_NA_OFF_BINBASE + FS_NA_TABLE_BYTES)
+#define FS_NA_OFF_TILEMAP (FS_NA_OFF_RSTART + FS_NA_ALIGN((FS_REGIONS + 1) * 4))
+#define FS_NA_OFF_LB0 (FS_NA_OFF_TILEMAP + FS_NA_ALIGN((unsigned long long)FS_NA_MAX_TILES * FS_TILE_DESC_WORDS * 4))
 #define FS_NA_OFF_LB1 (FS_NA_OFF_LB0 + FS_NA_LB_BYTES)
 #define FS_NA_OFF_S1K (FS_NA_OFF_LB1 + FS_NA_LB_BYTES)
 #define FS_NA_OFF_S2K (FS_NA_OFF_S1K + (unsigned long long)FS_NA_MAX_KEYS * 8)
 #define FS_NA_OFF_S1V (FS_NA_OFF_S2K + (unsigned long long)FS_NA_MAX_KEYS * 8)
 #define FS_NA_OFF_S2V (FS_NA_OFF_S1V + (unsigned long long)FS_NA_MAX_KEYS * 4)
 #define FS_NA_SCRATCH_BYTES (FS_NA_OFF_S2V + (unsigned long long)FS_NA_MAX_KEYS * 4)
-// bytes that must be zero before the first sort (histogram, and the
-// schedule with the upsweep's ticket); every sort leaves them zero again
-#define FS_NA_ZERO_BYTES FS_NA_OFF_LB0
+// bytes that must be zero before the first sort (histogram copies, the
+// schedule with its ticket, the region cursors); every sort leaves them zero
+#define FS_NA_ZERO_BYTES FS_NA_OFF_BINBASE
 
 // Kernel argument block, passed by value to every kernel.
 typedef struct FsArgs {
@@ -223,13 +261,18 @@ typedef struct FsArgs {
     uint64_t keys;              // caller keys (in place for KEYS/PAIRS; read-only for ARGSORT)
     uint64_t vals;              // caller values (PAIRS) or output indices (ARGSORT)
     uint64_t s1k, s2k, s1v, s2v;   // scratch ping-pong buffers
-    uint64_t hist;              // u32 [digits][256], zero between sorts
+    uint64_t hist;              // u32 [FS_HIST_SLOTS][FS_MAX_DIGITS][256], zero between sorts
     uint64_t binbase;           // u32 [digits][256]
     uint64_t lookback0, lookback1;  // [num_tiles][256] tile entries (u32, or u64 when wide),
                                     // then u32 [groups][256] group entries; alternate per pass
     uint64_t plan;              // u32[FS_PLAN_WORDS] schedule
     uint64_t status;            // u32, host-visible error bits
     uint64_t stats;             // u64[FS_STAT_SLOTS][FS_STAT_COUNT] look-back counters, or 0 when off
+    uint64_t cursors;           // u32[FS_REGIONS] region fill cursors of the fused pass (zero between sorts)
+    uint64_t rstart;            // u32[FS_REGIONS + 1] virtual start of each region (fused pass's schedule step)
+    uint64_t tilemap;           // u32[num_tiles][4] tile descriptors of the region layout (fused pass's schedule step)
+    uint32_t region_cap;        // keys per region (fused path), else 0
+    uint32_t fused;             // 1: the sort starts with the fused first pass (keys-only)
 } FsArgs;
 
 // Look-back statistics (accumulated only when FsArgs.stats is set).

@@ -35,7 +35,11 @@ KEY_SIZE = {"u32": 4, "i32": 4, "f32": 4, "u64": 8, "i64": 8, "f64": 8}   # Sort
 OP_SORT, OP_ARGSORT, OP_PAIRS = 0, 1, 2
 NO_ALLOC_MAX_KEYS = 1 << 20          # FS_NO_ALLOC_MAX_KEYS
 # fs_test_option and the FS_FAULT_* codes (include/forge_sort.h, csrc/fs_params.h)
-TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT = 0, 1, 2
+TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT, TEST_FUSED = 0, 1, 2, 3
+FUSED_BY_SIZE, FUSED_NEVER, FUSED_ALWAYS = 0, 1, 2       # TEST_FUSED values
+FUSED_MIN_KEYS = 1 << 25                                 # FS_FUSED_MIN_KEYS
+# fs_sorter_first_pass: how the last sort began
+FIRST_HISTOGRAM, FIRST_FUSED, FIRST_FUSED_OVERFLOW = 0, 1, 2
 FAULT_NONE, FAULT_BAD_DIGITS, FAULT_BAD_BUFFER, FAULT_EXTRA_BLOCK, FAULT_STALL_TILE = 0, 1, 2, 3, 4
 
 FS_OK = 0
@@ -129,6 +133,7 @@ def _load():
         "fs_reserve": ([vp, i, i, u64], i),
         "fs_allow_scratch_growth": ([vp], i),
         "fs_sorter_set_test_option": ([vp, i, u64], i),
+        "fs_sorter_first_pass": ([vp, u32p], i),
         "fs_synchronize": ([vp], i),
         "fs_last_pass_info": ([vp, u32p, u32p], i),
         "fs_set_profiling": ([vp, i], i),
@@ -379,9 +384,18 @@ class GpuSorter:
 
     def set_test_option(self, option, value):
         """Testing hooks (TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU,
-        TEST_INJECT_FAULT): reach layouts the product uses only at sizes too
-        large for a test, or inject a device-side fault (emulator builds)."""
+        TEST_INJECT_FAULT, TEST_FUSED): reach layouts the product uses only
+        at sizes too large for a test, choose the first pass, or inject a
+        device-side fault (emulator builds)."""
         self._check(_load().fs_sorter_set_test_option(self._h, option, value))
+
+    def first_pass(self):
+        """How the last sort began: FIRST_HISTOGRAM, FIRST_FUSED (the fused
+        first pass, regions used) or FIRST_FUSED_OVERFLOW (a region overflowed;
+        stable passes over the caller's keys followed)."""
+        k = ctypes.c_uint32()
+        self._check(_load().fs_sorter_first_pass(self._h, ctypes.byref(k)))
+        return k.value
 
     def device_synchronize(self):
         """Wait for everything on the device (hipDeviceSynchronize)."""

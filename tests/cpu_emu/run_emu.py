@@ -50,6 +50,11 @@ def keys_for(kind, n, dist, seed):
         # one varying digit above the lowest: the caller's keys are copied to
         # scratch first and the single pass writes them back
         b = (g.integers(0, 256, size=n, dtype=BITS[kind]) << BITS[kind](8)).astype(BITS[kind])
+    elif dist == "skew0":
+        # lowest byte 3 or 200, the rest uniform: the fused first pass's
+        # regions of those two digit values overflow
+        b = g.integers(0, 1 << (64 if wide else 32), size=n, dtype=BITS[kind], endpoint=False)
+        b = (b & ~BITS[kind](0xFF)) | np.where(g.integers(0, 2, size=n) == 0, 3, 200).astype(BITS[kind])
     elif dist == "zipf":
         # a dominant bin: Zipf(1.1) ranks below 2^20 (most keys small, digit 1
         # and 2 mostly zero), as in the pairs benchmark config
@@ -210,7 +215,39 @@ def check_no_alloc(sorter, kind, n, dist, seed):
     return ok
 
 
+# the fused first pass of keys-only 32-bit sorts: by size (the default), or
+# forced on for every case of a run (EMU_TEST_FUSED=2)
+FUSED_MODE = int(os.environ.get("EMU_TEST_FUSED", "0"))
+FIRST_PASS = {"fused": forge_sort.FIRST_FUSED, "fusedover": forge_sort.FIRST_FUSED_OVERFLOW,
+              "nofused": forge_sort.FIRST_HISTOGRAM}
+
+
+def check_first_pass(sorter, op, kind, n, dist, seed):
+    """A keys-only sort, exact, that began the way the case names
+    (fs_sorter_first_pass), with the fused first pass at every size, or
+    ("nofused") never."""
+    keys = keys_for(kind, n, dist, seed)
+    sorter.set_test_option(forge_sort.TEST_FUSED,
+                           forge_sort.FUSED_NEVER if op == "nofused" else forge_sort.FUSED_ALWAYS)
+    try:
+        ok = sorted_ok(sorter, kind, keys)
+        first = sorter.first_pass()
+        passes, mask = sorter.last_pass_info()
+    finally:
+        sorter.set_test_option(forge_sort.TEST_FUSED, FUSED_MODE)
+    if first != FIRST_PASS[op]:
+        print(f"  first pass {first}, expected {FIRST_PASS[op]}", flush=True)
+        ok = False
+    if dist == "same" and passes != 0:
+        print(f"  equal keys ran {passes} passes", flush=True)
+        ok = False
+    print(f"{'PASS' if ok else 'FAIL'} {op} {kind} n={n} {dist} passes={passes} mask={mask:#x}", flush=True)
+    return ok
+
+
 def check(sorter, op, kind, n, dist, seed):
+    if op in FIRST_PASS:
+        return check_first_pass(sorter, op, kind, n, dist, seed)
     if op == "noalloc":
         ok = check_no_alloc(sorter, kind, n, dist, seed)
         print(f"{'PASS' if ok else 'FAIL'} {op} {kind} n={n}", flush=True)
@@ -259,6 +296,7 @@ def main():
         sorter.set_test_option(forge_sort.TEST_WIDE_LOOKBACK, 1)
     if os.environ.get("EMU_TEST_UPSWEEP_PER_CU"):
         sorter.set_test_option(forge_sort.TEST_UPSWEEP_BLOCKS_PER_CU, int(os.environ["EMU_TEST_UPSWEEP_PER_CU"]))
+    sorter.set_test_option(forge_sort.TEST_FUSED, FUSED_MODE)
     print("tiles", sorter.tile_config(), flush=True)
     ok = True
     for spec in sys.argv[2:]:

@@ -74,3 +74,13 @@ def test_no_alloc_limits_match_the_scratch_layout(tmp_path):
                         "-I", os.path.join(ROOT, "include"), str(src), "-o", str(tmp_path / "na")],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_python_constants_match_the_header():
+    """The Python binding's copies of header constants equal the header's."""
+    import re
+    import forge_sort
+    h = open(os.path.join(ROOT, "include", "forge_sort.h")).read()
+    val = lambda name: int(re.search(r"#define %s (\d+)u" % name, h).group(1))
+    assert forge_sort.FUSED_MIN_KEYS == val("FS_FUSED_MIN_KEYS")
+    assert forge_sort.NO_ALLOC_MAX_KEYS == val("FS_NO_ALLOC_MAX_KEYS")

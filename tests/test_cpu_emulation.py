@@ -85,6 +85,36 @@ def test_emulated_production_tiles(emulator):
 
 
 
+FUSED_SMALL = [
+    # regions used: every digit varies; ragged; tiny; only digit 0 varies (the
+    # regions copied back); two digits vary
+    "fused:u32:9000:uniform:1", "fused:f32:20000:uniform:2", "fused:u32:1025:uniform:3",
+    "fused:i32:2:uniform:4", "fused:i32:5000:byte0:5", "fused:u32:3000:low12:6",
+    # a region overflows (skewed lowest byte; lowest byte constant), or every
+    # digit is constant: stable passes over the caller's keys
+    "fusedover:u32:9000:skew0:7", "fusedover:f32:6000:byte1:8", "fusedover:u32:50:same:9",
+    "fusedover:u32:9000:same:10",
+    # the testing hook: the histogram read instead
+    "nofused:u32:9000:uniform:11", "nofused:i32:4099:byte0:12",
+]
+
+
+def test_emulated_fused_first_pass(emulator):
+    """Keys-only 32-bit sorts start with the fused first pass: with small
+    tiles a tile of the next pass spans dozens of regions, with production
+    tiles a region spans several tiles; look-back groups of two tiles follow
+    it in the groups build."""
+    run_cases("small", FUSED_SMALL)
+    run_cases("prod", ["fused:u32:100000:uniform:1", "fused:f32:17665:uniform:2", "fused:u32:40000:byte0:3",
+                       "fusedover:u32:40000:skew0:4", "nofused:u32:40000:uniform:5"])
+    run_cases("groups", ["fused:u32:70000:uniform:1", "fusedover:i32:30000:skew0:2"], env={"EMU_CUS": "8"})
+    # regions larger than tiles: one- and two-region tile descriptors (and
+    # more-region tiles where a region holds fewer keys than a tile)
+    run_cases("regions", ["fused:u32:60000:uniform:1", "fused:f32:150001:uniform:2", "fused:i32:50000:byte0:3",
+                          "fused:u32:40000:low12:4", "fusedover:u32:60000:skew0:5", "noalloc:u32:60000:uniform:6",
+                          "sort:u64:9000:uniform:7", "pairs:u32:9000:uniform:8"], env={"EMU_TEST_FUSED": "2"})
+
+
 def test_emulated_lookback_groups(emulator):
     """Look-back groups of two tiles, one tile entry per round trip, eight
     emulated CUs: most look-backs cross several groups, and predecessors are
@@ -137,6 +167,10 @@ def test_emulated_device_error_guards(emulator):
                          "fault_tile:u32:5000:uniform:5", "fault_tile:f64:3000:uniform:6",
                          "fault_stall:u32:9000:uniform:7", "fault_stall:u64:5000:uniform:8"],
               env={"EMU_CUS": "8"})
+    # the same guards behind the fused first pass of keys-only 32-bit sorts
+    run_cases("faults", ["fault_digits:u32:5000:uniform:1", "fault_buffer:f32:5000:uniform:3",
+                         "fault_tile:u32:5000:uniform:5", "fault_stall:i32:9000:uniform:7"],
+              env={"EMU_CUS": "8", "EMU_TEST_FUSED": "2"})
 
 
 def test_emulated_held_xcd_queue(emulator):
@@ -151,12 +185,14 @@ def test_emulated_no_alloc_entry_point(emulator):
     """fs_encode_no_alloc (static scratch, no allocation) gives fs_encode's
     results for every op, on two calls in a row, the second smaller."""
     run_cases("small", ["noalloc:u32:9000:uniform:1", "noalloc:f64:5000:few:2", "noalloc:i32:4099:zipf:3"])
+    run_cases("small", ["noalloc:u32:9000:uniform:4", "noalloc:f32:6000:skew0:5"], env={"EMU_TEST_FUSED": "2"})
 
 
 def test_emulated_capture_rules(emulator):
     """A sort enqueued on a capturing stream fits the reserved scratch or is
     refused; after a capture, growth is refused until fs_allow_scratch_growth."""
     run_cases("small", ["capture:u32:3000:uniform:1", "capture:f64:2000:uniform:2"])
+    run_cases("small", ["capture:u32:3000:uniform:3"], env={"EMU_TEST_FUSED": "2"})
 
 
 def test_emulated_sanitizers(emulator):
@@ -168,6 +204,7 @@ def test_emulated_sanitizers(emulator):
     # ASan reports its own faults: the emulator's guard-page handler stays off
     run_cases("san", ["sort:u32:5000:uniform:1", "sort:f32:3001:uniform:3", "argsort:i32:2000:few:7",
                       "pairs:f64:2500:uniform:12", "sort:u32:5000:byte0:31", "sort:u32:9000:zipf:28",
-                      "gather:u32:3000:uniform:26"],
-              timeout=600, env={"LD_PRELOAD": libasan, "EMU_NO_SEGV_HANDLER": "1", "EMU_CUS": "4",
+                      "gather:u32:3000:uniform:26", "fused:u32:9000:uniform:40", "fusedover:u32:9000:skew0:41",
+                      "fused:u32:5000:byte0:42"],
+              timeout=600, env={"LD_PRELOAD": libasan, "EMU_NO_SEGV_HANDLER": "1", "EMU_CUS": "4", "EMU_TEST_FUSED": "2",
                                 "ASAN_OPTIONS": "detect_leaks=0:detect_stack_use_after_return=0"})

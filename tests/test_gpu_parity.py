@@ -130,6 +130,9 @@ def make_keys(kind, n, dist, seed):
         b = g.integers(0, 256, size=n, dtype=BITS[kind])
     elif dist == "byte1":       # one varying digit above it: copy to scratch, then single pass
         b = (g.integers(0, 256, size=n, dtype=BITS[kind]) << BITS[kind](8)).astype(BITS[kind])
+    elif dist == "skew0":       # lowest byte 3 or 200, the rest uniform
+        b = g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False)
+        b = (b & ~BITS[kind](0xFF)) | np.where(g.integers(0, 2, size=n) == 0, 3, 200).astype(BITS[kind])
     else:
         raise ValueError(dist)
     keys = b.view(NP[kind])
@@ -286,6 +289,75 @@ def test_slice_staging_ragged_chunks(sorter):
     check_argsort(sorter, "i64", datagen.uniform_i64(2 * chunk_u64 + 1, seed=134))
     check_sort(sorter, "f64", datagen.normal_f64(chunk_u64 + 3, seed=135))
     check_sort(sorter, "u32", datagen.uniform_u32(5, seed=136))
+
+
+# ---- the fused first pass of keys-only 32-bit sorts ----------------------------------
+
+FUSED_CASES = [
+    # its regions feed the next pass: every digit varies; only digit 0 (the
+    # regions copied back); digits 0 and 1
+    (1_000_003, "uniform", 1), (16_777_216, "uniform", 1), (300_007, "byte0", 1), (2_000_000, "lowbits", 1),
+    # a region overflows (skewed lowest byte; lowest byte constant) or every
+    # digit is constant: the standard schedule over the caller's keys
+    (1_000_000, "skew0", 2), (500_000, "byte1", 2), (100_003, "same", 2),
+]
+
+
+@pytest.mark.parametrize("kind", ["u32", "i32", "f32"])
+@pytest.mark.parametrize("n,dist,expect", FUSED_CASES)
+def test_fused_first_pass(sorter, kind, n, dist, expect):
+    """Keys-only 32-bit sorts begin with the fused first pass (one read that
+    counts the upper digits and scatters by the lowest into regions), here
+    forced at every size: exact against the oracle on both of its schedules,
+    through the slice and buffer APIs; the histogram read gives the same keys."""
+    from forge_sort import FIRST_HISTOGRAM, FUSED_ALWAYS, FUSED_BY_SIZE, FUSED_NEVER, TEST_FUSED
+    keys = make_keys(kind, n, dist, seed=900 + n % 97)
+    sorter.set_test_option(TEST_FUSED, FUSED_ALWAYS)
+    try:
+        check_sort(sorter, kind, keys)
+        assert sorter.first_pass() == expect
+        passes, mask = sorter.last_pass_info()
+        if dist == "same":
+            assert (passes, mask) == (0, 0)
+        elif dist == "uniform":
+            assert (passes, mask) == (4, 0xF)
+        check_buffer(sorter, kind, keys)
+        assert sorter.first_pass() == expect
+        sorter.set_test_option(TEST_FUSED, FUSED_NEVER)
+        check_sort(sorter, kind, keys)
+        assert sorter.first_pass() == FIRST_HISTOGRAM
+        assert sorter.last_pass_info() == (passes, mask)
+    finally:
+        sorter.set_test_option(TEST_FUSED, FUSED_BY_SIZE)
+
+
+@pytest.mark.parametrize("n,expect", [(1 << 25, 1), ((1 << 25) - 1, 0), (1 << 20, 0)])
+def test_fused_first_pass_by_size(sorter, n, expect):
+    """By default the fused first pass starts at FS_FUSED_MIN_KEYS keys."""
+    keys = datagen.uniform_u32(n, seed=950)
+    check_buffer(sorter, "u32", keys)
+    assert sorter.first_pass() == expect
+
+
+def test_fused_first_pass_2_31_keys(sorter):
+    """The largest fused sort (n = 2^31, regions of S1 just below 2^32 keys
+    in all) and one key more (the histogram read): ascending, same multiset."""
+    for n, expect in ((1 << 31, 1), ((1 << 31) + 1, 0)):
+        keys = datagen.uniform_u32(n, seed=501)
+        k64 = keys.astype(np.uint64)
+        s_sum, s_sq, s_xor = int(k64.sum()), int((k64 * k64).sum()), int(np.bitwise_xor.reduce(keys))
+        del k64
+        buf = sorter.alloc_sort_buffer("u32", n)
+        buf.copy_from_slice(keys)
+        del keys
+        sorter.sort_buffer(buf)
+        assert sorter.first_pass() == expect
+        out = buf.as_slice()
+        buf.free()
+        assert bool(np.all(out[1:] >= out[:-1])), "not ascending"
+        o64 = out.astype(np.uint64)
+        assert (int(o64.sum()), int((o64 * o64).sum()), int(np.bitwise_xor.reduce(out))) == (s_sum, s_sq, s_xor)
+        del out, o64
 
 
 # ---- BASELINE.json configurations at full size ------------------------------------
@@ -596,41 +668,52 @@ def hip_stream():
     hip.hipStreamDestroy(st)
 
 
-def test_graph_capture_replays(hip_stream):
+@pytest.mark.parametrize("op", ["pairs", "sort"])
+def test_graph_capture_replays(hip_stream, op):
     """The sort is capturable into a HIP graph: fs_encode on a capturing stream
     records kernel launches only (no memset; the scratch has grown beforehand,
-    and the kernels reset the histogram, the upsweep ticket and the look-back
-    entries themselves).  Each replay sorts new data with its own device-side
-    schedule (4, 4, 2 and 1 passes), eager sorts run between the replays, and
-    every replay matches the oracle."""
+    and the kernels reset the histogram copies, the region cursors, the ticket
+    and the look-back entries themselves).  Each replay sorts new data with its
+    own device-side schedule (pairs: 4, 4, 2 and 1 passes; keys only: the
+    fused first pass's regions, an overflowing region, equal keys, only digit
+    0 varying), eager sorts run between the replays, and every replay matches
+    the oracle."""
     import ctypes
-    from forge_sort import OP_PAIRS, GpuSorter
+    from forge_sort import FUSED_ALWAYS, OP_PAIRS, OP_SORT, TEST_FUSED, GpuSorter
     hip = ctypes.CDLL("libamdhip64.so.7")
     st = ctypes.c_void_p(hip_stream)
     s = GpuSorter.with_context(0, hip_stream)
     graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    pairs = op == "pairs"
+    code = OP_PAIRS if pairs else OP_SORT
+    s.set_test_option(TEST_FUSED, FUSED_ALWAYS)       # keys only: the fused first pass at this size
     try:
-        n = 1_000_003
+        n, n_other = 1_000_003, 200_001
         g = np.random.Generator(np.random.PCG64(904))
         kb, vb = s.alloc_sort_buffer("u32", n), s.alloc_sort_buffer("u32", n)
         kb.copy_from_slice(make_keys("u32", n, "uniform", seed=900))
         vb.copy_from_slice(g.integers(0, 1 << 32, size=n, dtype=np.uint32))
-        s.encode(OP_PAIRS, "u32", kb.device_ptr(), vb.device_ptr(), n, stream=hip_stream)
+        s.encode(code, "u32", kb.device_ptr(), vb.device_ptr(), n, stream=hip_stream)
+        s.reserve(OP_SORT, "u32", n_other)    # the eager sorts between the replays
         s.synchronize()                       # scratch grown: the captured sort allocates nothing
         assert hip.hipStreamBeginCapture(st, 0) == 0
-        s.encode(OP_PAIRS, "u32", kb.device_ptr(), vb.device_ptr(), n, stream=hip_stream)
+        s.encode(code, "u32", kb.device_ptr(), vb.device_ptr(), n, stream=hip_stream)
         assert hip.hipStreamEndCapture(st, ctypes.byref(graph)) == 0
         assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
-        for r, dist in enumerate(["uniform", "few", "lowbits", "byte1"]):
+        dists = ["uniform", "few", "lowbits", "byte1"] if pairs else ["uniform", "skew0", "same", "byte0", "uniform"]
+        for r, dist in enumerate(dists):
             keys = make_keys("u32", n, dist, seed=910 + r)
             vals = g.integers(0, 1 << 32, size=n, dtype=np.uint32)
             kb.copy_from_slice(keys)
             vb.copy_from_slice(vals)
             assert hip.hipGraphLaunch(exe, st) == 0
             assert hip.hipStreamSynchronize(st) == 0
-            ek, ev = oracle.sort_pairs("u32", keys, vals)
-            assert np.array_equal(kb.as_slice(), ek) and np.array_equal(vb.as_slice(), ev), f"replay {r} ({dist})"
-            other = make_keys("u32", 200_001, "uniform", seed=950 + r)   # eager work between replays
+            if pairs:
+                ek, ev = oracle.sort_pairs("u32", keys, vals)
+                assert np.array_equal(kb.as_slice(), ek) and np.array_equal(vb.as_slice(), ev), f"replay {r} ({dist})"
+            else:
+                assert np.array_equal(kb.as_slice(), oracle.sort("u32", keys)), f"replay {r} ({dist})"
+            other = make_keys("u32", n_other, "uniform", seed=950 + r)   # eager work between replays
             got = other.copy()
             s.sort_u32(got)
             assert np.array_equal(got, oracle.sort("u32", other))
