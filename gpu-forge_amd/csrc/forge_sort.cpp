@@ -295,11 +295,11 @@ static uint64_t region_cap(uint64_t n, uint32_t tile) {
     return (3 * keys) / (2 * FS_RADIX) + 64;
 }
 
-// Keys-only sorts of 32-bit keys start with the fused first pass (no
+// Keys-only sorts (32- and 64-bit keys) start with the fused first pass (no
 // histogram read); S1 then holds FS_REGIONS regions, which must stay below
 // 2^32 keys (n <= 2^31 keeps them below 1.5 n + 2^17).
 static bool fused_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
-    if (op != FS_OP_SORT || key64(t) || n > (1ull << 31) || s->fused_mode == 1u) return false;
+    if (op != FS_OP_SORT || n > (1ull << 31) || s->fused_mode == 1u) return false;
     return s->fused_mode == 2u || n >= FS_FUSED_MIN_KEYS;
 }
 

@@ -222,20 +222,21 @@ typedef enum fs_test_option {
     FS_TEST_WIDE_LOOKBACK = 0,          /* value != 0: 64-bit look-back entries for any n */
     FS_TEST_UPSWEEP_BLOCKS_PER_CU = 1,  /* histogram blocks per CU, 1..64 (0 = by key width) */
     FS_TEST_INJECT_FAULT = 2,           /* FS_FAULT_* (fault-injection builds only) */
-    FS_TEST_FUSED = 3                   /* keys-only 32-bit sorts begin with the fused first
-                                           pass: 0 = from FS_FUSED_MIN_KEYS keys on (the
-                                           default), 1 = never, 2 = at every size */
+    FS_TEST_FUSED = 3                   /* keys-only sorts begin with the fused first pass:
+                                           0 = from FS_FUSED_MIN_KEYS keys on (the default),
+                                           1 = never, 2 = at every size */
 } fs_test_option;
 fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t value);
 
-/* Keys-only sorts of 32-bit keys from this many keys on (up to 2^31) begin
+/* Keys-only sorts (any key type) from this many keys on (up to 2^31) begin
  * with the fused first pass; below it the histogram read and the first
- * digit pass cost less than the fused pass and the region read after it. */
+ * digit pass cost less than the fused pass and the region read after it
+ * (measured for u32 and u64 keys). */
 #define FS_FUSED_MIN_KEYS 33554432u
 
-/* How the last completed sort began: 0 = the histogram read (64-bit keys,
- * argsort, pairs, and keys-only sorts outside the fused range), 1 = the fused
- * first pass of keys-only 32-bit sorts, its regions read by the next pass,
+/* How the last completed sort began: 0 = the histogram read (argsort, pairs,
+ * and keys-only sorts outside the fused range), 1 = the fused first pass of a
+ * keys-only sort, its regions read by the next pass,
  * 2 = the fused first pass, then stable passes over the caller's keys (a
  * region overflowed on a skewed lowest byte, or every digit is constant). */
 fs_status fs_sorter_first_pass(fs_sorter *s, uint32_t *kind);

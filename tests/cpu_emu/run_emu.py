@@ -215,7 +215,7 @@ def check_no_alloc(sorter, kind, n, dist, seed):
     return ok
 
 
-# the fused first pass of keys-only 32-bit sorts: by size (the default), or
+# the fused first pass of keys-only sorts: by size (the default), or
 # forced on for every case of a run (EMU_TEST_FUSED=2)
 FUSED_MODE = int(os.environ.get("EMU_TEST_FUSED", "0"))
 FIRST_PASS = {"fused": forge_sort.FIRST_FUSED, "fusedover": forge_sort.FIRST_FUSED_OVERFLOW,

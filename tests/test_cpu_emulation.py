@@ -96,23 +96,28 @@ FUSED_SMALL = [
     "fusedover:u32:9000:same:10",
     # the testing hook: the histogram read instead
     "nofused:u32:9000:uniform:11", "nofused:i32:4099:byte0:12",
+    # 64-bit keys: seven upper digits counted, regions of 8-byte keys
+    "fused:u64:9000:uniform:13", "fused:f64:5001:uniform:14", "fused:i64:3000:byte0:15",
+    "fusedover:u64:6000:skew0:16", "fusedover:f64:40:same:17", "nofused:u64:3000:uniform:18",
 ]
 
 
 def test_emulated_fused_first_pass(emulator):
-    """Keys-only 32-bit sorts start with the fused first pass: with small
+    """Keys-only sorts (32- and 64-bit keys) start with the fused first pass: with small
     tiles a tile of the next pass spans dozens of regions, with production
     tiles a region spans several tiles; look-back groups of two tiles follow
     it in the groups build."""
     run_cases("small", FUSED_SMALL)
     run_cases("prod", ["fused:u32:100000:uniform:1", "fused:f32:17665:uniform:2", "fused:u32:40000:byte0:3",
-                       "fusedover:u32:40000:skew0:4", "nofused:u32:40000:uniform:5"])
+                       "fusedover:u32:40000:skew0:4", "nofused:u32:40000:uniform:5", "fused:u64:30000:uniform:6",
+                       "fused:i64:7681:uniform:7"])
     run_cases("groups", ["fused:u32:70000:uniform:1", "fusedover:i32:30000:skew0:2"], env={"EMU_CUS": "8"})
     # regions larger than tiles: one- and two-region tile descriptors (and
     # more-region tiles where a region holds fewer keys than a tile)
     run_cases("regions", ["fused:u32:60000:uniform:1", "fused:f32:150001:uniform:2", "fused:i32:50000:byte0:3",
                           "fused:u32:40000:low12:4", "fusedover:u32:60000:skew0:5", "noalloc:u32:60000:uniform:6",
-                          "sort:u64:9000:uniform:7", "pairs:u32:9000:uniform:8"], env={"EMU_TEST_FUSED": "2"})
+                          "sort:u64:9000:uniform:7", "pairs:u32:9000:uniform:8", "fused:u64:20000:uniform:9",
+                          "fused:f64:9000:low12:10"], env={"EMU_TEST_FUSED": "2"})
 
 
 def test_emulated_lookback_groups(emulator):

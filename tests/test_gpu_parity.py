@@ -291,7 +291,7 @@ def test_slice_staging_ragged_chunks(sorter):
     check_sort(sorter, "u32", datagen.uniform_u32(5, seed=136))
 
 
-# ---- the fused first pass of keys-only 32-bit sorts ----------------------------------
+# ---- the fused first pass of keys-only sorts -----------------------------------------
 
 FUSED_CASES = [
     # its regions feed the next pass: every digit varies; only digit 0 (the
@@ -303,10 +303,10 @@ FUSED_CASES = [
 ]
 
 
-@pytest.mark.parametrize("kind", ["u32", "i32", "f32"])
+@pytest.mark.parametrize("kind", ["u32", "i32", "f32", "u64", "i64", "f64"])
 @pytest.mark.parametrize("n,dist,expect", FUSED_CASES)
 def test_fused_first_pass(sorter, kind, n, dist, expect):
-    """Keys-only 32-bit sorts begin with the fused first pass (one read that
+    """Keys-only sorts begin with the fused first pass (one read that
     counts the upper digits and scatters by the lowest into regions), here
     forced at every size: exact against the oracle on both of its schedules,
     through the slice and buffer APIs; the histogram read gives the same keys."""
@@ -320,7 +320,7 @@ def test_fused_first_pass(sorter, kind, n, dist, expect):
         if dist == "same":
             assert (passes, mask) == (0, 0)
         elif dist == "uniform":
-            assert (passes, mask) == (4, 0xF)
+            assert (passes, mask) == ((8, 0xFF) if kind.endswith("64") else (4, 0xF))
         check_buffer(sorter, kind, keys)
         assert sorter.first_pass() == expect
         sorter.set_test_option(TEST_FUSED, FUSED_NEVER)
