@@ -40,11 +40,11 @@ struct ProfEntry {
 const char* const kKernelNames[] = {
     "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
-    "fs_scratch_address", "fs_first_k32", "fs_first_k64",
+    "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
-    K_COUNT
+    K_SAMPLE32, K_SAMPLE64, K_COUNT
 };
 
 }  // namespace
@@ -64,6 +64,7 @@ struct fs_sorter {
     uint32_t* binbase = nullptr;    // [8][256]
     uint32_t* cursors = nullptr;    // [FS_REGIONS] region cursors of the fused pass, zero between sorts
     uint32_t* rstart = nullptr;     // [FS_REGIONS + 1] region starts
+    uint32_t* rtable = nullptr;     // [FS_RTABLE_WORDS] region bases, total and caps of the fused pass
     uint32_t* plan = nullptr;       // u32[FS_PLAN_WORDS] device-side schedule
     uint32_t* status = nullptr;     // pinned host word written by kernels on device errors
     unsigned long long* stats = nullptr;   // device u64[FS_STAT_COUNT]
@@ -282,24 +283,25 @@ static int variant_of(fs_op op, fs_key_type t) {
 // than 30 bits, or when a test forces that layout.
 static bool wide_lookback(const fs_sorter* s, uint64_t n) { return n >= FS_LB_WIDE_KEYS || s->force_wide; }
 
-// Keys per region of the fused first pass (fs_params.h): tile t writes the
-// regions of group (t / FS_XCD_TILES) % FS_SUBS, so a region receives about
-// 1/FS_RADIX of its group's keys; the cap is 1.5x that share of the largest
-// group, plus a margin, so that uniform keys never overflow a region.
-static uint64_t region_cap(uint64_t n, uint32_t tile) {
+// Keys of the fullest region group of the fused first pass (fs_params.h):
+// tile t writes the regions of group (t / FS_XCD_TILES) % FS_SUBS.  The
+// regions of a group share its keys by digit value; fs_region_sample_* sizes
+// them from a sample, within FS_FUSED_S1_KEYS of S1.
+static uint64_t fused_sub_keys(uint64_t n, uint32_t tile) {
     const uint64_t tiles = (n + tile - 1) / tile;
     const uint64_t runs = (tiles + FS_XCD_TILES - 1) / FS_XCD_TILES;    // runs of FS_XCD_TILES tiles
     const uint64_t most = (runs + FS_SUBS - 1) / FS_SUBS;              // group 0 has the most runs
     uint64_t keys = most * FS_XCD_TILES * tile;
     if (keys > n) keys = n;
-    return (3 * keys) / (2 * FS_RADIX) + 64;
+    return keys;
 }
 
 // Keys-only sorts (32- and 64-bit keys) start with the fused first pass (no
 // histogram read); S1 then holds FS_REGIONS regions, which must stay below
-// 2^32 keys (n <= 2^31 keeps them below 1.5 n + 2^17).
+// 2^32 keys (n <= 2^31 keeps them below 1.875 n + 2^17).
 static bool fused_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
     if (op != FS_OP_SORT || n > (1ull << 31) || s->fused_mode == 1u) return false;
+    if (FS_FUSED_S1_KEYS(fused_sub_keys(n, s->tile[variant_of(op, t)])) >= (1ull << 32)) return false;
     return s->fused_mode == 2u || n >= FS_FUSED_MIN_KEYS;
 }
 
@@ -314,7 +316,7 @@ static fs_status reserve(fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
     const uint64_t num_tiles = (n + tile - 1) / tile;
     fs_status r;
     const bool fused = fused_path(s, op, t, n);
-    if ((r = ensure(s, s->s1k, (fused ? FS_REGIONS * region_cap(n, tile) : n) * kb)) != FS_OK) return r;
+    if ((r = ensure(s, s->s1k, (fused ? FS_FUSED_S1_KEYS(fused_sub_keys(n, tile)) : n) * kb)) != FS_OK) return r;
     if ((r = ensure(s, s->s2k, n * kb)) != FS_OK) return r;
     if (fused && (r = ensure(s, s->tilemap, num_tiles * FS_TILE_DESC_WORDS * 4)) != FS_OK) return r;
     if (op != FS_OP_SORT) {
@@ -330,7 +332,7 @@ static fs_status reserve(fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
 // Device addresses of the scratch a sort uses: the sorter's own grow-only
 // buffers, or the static array of fs_encode_no_alloc.
 struct ScratchSet {
-    uint64_t s1k, s2k, s1v, s2v, lb0, lb1, hist, binbase, plan, cursors, rstart, tilemap;
+    uint64_t s1k, s2k, s1v, s2v, lb0, lb1, hist, binbase, plan, cursors, rstart, tilemap, rtable;
 };
 
 static ScratchSet sorter_scratch(const fs_sorter* s) {
@@ -339,14 +341,16 @@ static ScratchSet sorter_scratch(const fs_sorter* s) {
                       (uint64_t)(uintptr_t)s->lb0.p, (uint64_t)(uintptr_t)s->lb1.p,
                       (uint64_t)(uintptr_t)s->hist, (uint64_t)(uintptr_t)s->binbase,
                       (uint64_t)(uintptr_t)s->plan, (uint64_t)(uintptr_t)s->cursors,
-                      (uint64_t)(uintptr_t)s->rstart, (uint64_t)(uintptr_t)s->tilemap.p};
+                      (uint64_t)(uintptr_t)s->rstart, (uint64_t)(uintptr_t)s->tilemap.p,
+                      (uint64_t)(uintptr_t)s->rtable};
 }
 
 static ScratchSet static_scratch(const fs_sorter* s) {
     const uint64_t p = (uint64_t)(uintptr_t)s->na_scratch;
     return ScratchSet{p + FS_NA_OFF_S1K, p + FS_NA_OFF_S2K, p + FS_NA_OFF_S1V, p + FS_NA_OFF_S2V,
                       p + FS_NA_OFF_LB0, p + FS_NA_OFF_LB1, p + FS_NA_OFF_HIST, p + FS_NA_OFF_BINBASE,
-                      p + FS_NA_OFF_PLAN, p + FS_NA_OFF_CURSORS, p + FS_NA_OFF_RSTART, p + FS_NA_OFF_TILEMAP};
+                      p + FS_NA_OFF_PLAN, p + FS_NA_OFF_CURSORS, p + FS_NA_OFF_RSTART, p + FS_NA_OFF_TILEMAP,
+                      p + FS_NA_OFF_RTABLE};
 }
 
 // no_alloc: the sort runs on the static scratch (fs_encode_no_alloc): nothing
@@ -394,8 +398,9 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     const ScratchSet sc = no_alloc ? static_scratch(s) : sorter_scratch(s);
     // the fused first pass, when its regions fit the scratch (the static
     // scratch's S1 holds FS_NA_MAX_KEYS 8-byte keys)
+    const uint64_t sub_keys = fused_sub_keys(n, tile);
     const bool fused = fused_path(s, op, t, n) &&
-                       (!no_alloc || FS_REGIONS * region_cap(n, tile) * kb <= (uint64_t)FS_NA_MAX_KEYS * 8);
+                       (!no_alloc || FS_FUSED_S1_KEYS(sub_keys) * kb <= (uint64_t)FS_NA_MAX_KEYS * 8);
 
     FsArgs a;
     memset(&a, 0, sizeof a);
@@ -433,8 +438,10 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.cursors = sc.cursors;
     a.rstart = sc.rstart;
     a.tilemap = sc.tilemap;
+    a.rtable = sc.rtable;
     a.fused = fused ? 1u : 0u;
-    a.region_cap = fused ? (uint32_t)region_cap(n, tile) : 0u;
+    a.sub_keys = fused ? (uint32_t)sub_keys : 0u;
+    a.s1_keys = fused ? (uint32_t)FS_FUSED_S1_KEYS(sub_keys) : 0u;
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 #ifdef FS_FAULT_INJECTION
@@ -444,6 +451,8 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
 
     void* args1[] = {&a};
     if (fused) {
+        if ((r = launch(s, key64(t) ? K_SAMPLE64 : K_SAMPLE32, 1, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK)
+            return r;
         unsigned grid = num_tiles;
 #ifdef FS_FAULT_INJECTION
         if (s->fault == FS_FAULT_EXTRA_BLOCK) grid += 1u;
@@ -577,6 +586,7 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
     const size_t tab = (size_t)FS_MAX_DIGITS * FS_RADIX * 4;
     if (hipMalloc(&s->hist, (size_t)FS_HIST_WORDS * 4) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||
         hipMalloc(&s->cursors, FS_REGIONS * 4) != hipSuccess || hipMalloc(&s->rstart, (FS_REGIONS + 1) * 4) != hipSuccess ||
+        hipMalloc(&s->rtable, FS_RTABLE_WORDS * 4) != hipSuccess ||
         hipMalloc(&s->plan, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc(&s->stats, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
@@ -630,6 +640,7 @@ void fs_sorter_free(fs_sorter* s) {
     if (s->hist) (void)hipFree(s->hist);
     if (s->cursors) (void)hipFree(s->cursors);
     if (s->rstart) (void)hipFree(s->rstart);
+    if (s->rtable) (void)hipFree(s->rtable);
     if (s->binbase) (void)hipFree(s->binbase);
     if (s->plan) (void)hipFree(s->plan);
     if (s->stats) (void)hipFree(s->stats);

@@ -150,8 +150,13 @@
 // keys once, counts the other digits for the later passes (the histogram read
 // a sort otherwise starts with), and scatters the keys by digit 0 into fixed
 // regions of scratch S1: FS_SUBS regions per digit value, region
-// k = digit * FS_SUBS + sub of FsArgs.region_cap keys at S1 + k * region_cap,
-// where sub is the XCD group of the tile.  A tile takes the space of each of
+// k = digit * FS_SUBS + sub at S1 + base[k], holding cap[digit] keys, where
+// sub is the XCD group of the tile.  The region table (base[k] for every
+// region, base[FS_REGIONS] = the regions' total, then cap[d] for every digit
+// value) is written just before the pass by fs_region_sample_*, from the
+// digit-0 histogram of a sample of the keys: a digit value's regions hold
+// 1.5x its estimated share of the fullest region group's keys (the share at
+// least a quarter of 1/256), plus a margin.  A tile takes the space of each of
 // its digit runs with one atomic on the region's cursor (an LSD sort's first
 // pass needs no order among equal digits), so the pass has no look-back.  The
 // region start table (virtual position of each region's first key, regions
@@ -162,6 +167,18 @@
 #define FS_SUBS 8
 #endif
 #define FS_REGIONS (FS_RADIX * FS_SUBS)
+// Region table words (bases, total, caps), and the sample: FS_SAMPLE_CHUNKS
+// runs of FS_SAMPLE_CHUNK consecutive keys spread evenly over the input (all
+// keys when there are fewer).
+#define FS_RTABLE_WORDS (FS_REGIONS + 1 + FS_RADIX)
+#define FS_RTABLE_CAPS (FS_REGIONS + 1)
+#define FS_SAMPLE_CHUNKS 256
+#define FS_SAMPLE_CHUNK 128
+// S1 keys the fused pass's regions may take for region groups of at most
+// sub_keys keys each: 1.5 x (1 + 256 / 1024) of FS_SUBS groups, plus the
+// margins and rounding of every region.
+#define FS_FUSED_S1_KEYS(sub_keys) ((15ull * (unsigned long long)(sub_keys) * FS_SUBS + 7ull) / 8ull + \
+                                    (unsigned long long)FS_REGIONS * 65ull)
 // Histogram table: FS_HIST_SLOTS copies of [FS_MAX_DIGITS][FS_RADIX]; the
 // fused pass's tiles fold their counts into copy (tile % FS_HIST_SLOTS), so
 // that no counter takes more than num_tiles / FS_HIST_SLOTS atomics.
@@ -234,7 +251,8 @@
 #define FS_NA_OFF_CURSORS (FS_NA_OFF_PLAN + FS_NA_ALIGN(FS_PLAN_WORDS * 4))
 #define FS_NA_OFF_BINBASE (FS_NA_OFF_CURSORS + FS_NA_ALIGN(FS_REGIONS * 4))
 #define FS_NA_OFF_RSTART (FS_NA_OFF_BINBASE + FS_NA_TABLE_BYTES)
-#define FS_NA_OFF_TILEMAP (FS_NA_OFF_RSTART + FS_NA_ALIGN((FS_REGIONS + 1) * 4))
+#define FS_NA_OFF_RTABLE (FS_NA_OFF_RSTART + FS_NA_ALIGN((FS_REGIONS + 1) * 4))
+#define FS_NA_OFF_TILEMAP (FS_NA_OFF_RTABLE + FS_NA_ALIGN(FS_RTABLE_WORDS * 4))
 #define FS_NA_OFF_LB0 (FS_NA_OFF_TILEMAP + FS_NA_ALIGN((unsigned long long)FS_NA_MAX_TILES * FS_TILE_DESC_WORDS * 4))
 #define FS_NA_OFF_LB1 (FS_NA_OFF_LB0 + FS_NA_LB_BYTES)
 #define FS_NA_OFF_S1K (FS_NA_OFF_LB1 + FS_NA_LB_BYTES)
@@ -271,8 +289,11 @@ typedef struct FsArgs {
     uint64_t cursors;           // u32[FS_REGIONS] region fill cursors of the fused pass (zero between sorts)
     uint64_t rstart;            // u32[FS_REGIONS + 1] virtual start of each region (fused pass's schedule step)
     uint64_t tilemap;           // u32[num_tiles][4] tile descriptors of the region layout (fused pass's schedule step)
-    uint32_t region_cap;        // keys per region (fused path), else 0
+    uint64_t rtable;            // u32[FS_RTABLE_WORDS] region bases, total and caps (fs_region_sample_*)
+    uint32_t sub_keys;          // keys of the fullest region group (fused path), else 0
     uint32_t fused;             // 1: the sort starts with the fused first pass (keys-only)
+    uint32_t s1_keys;           // keys S1 holds (fused path: the regions' budget), else 0
+    uint32_t reserved0;
 } FsArgs;
 
 // Look-back statistics (accumulated only when FsArgs.stats is set).

@@ -312,6 +312,8 @@ void fs_onesweep_any_k32(FsArgs, uint32_t);
 void fs_onesweep_any_k64(FsArgs, uint32_t);
 void fs_first_k32(FsArgs);
 void fs_first_k64(FsArgs);
+void fs_region_sample_k32(FsArgs);
+void fs_region_sample_k64(FsArgs);
 void fs_iota(uint32_t*, uint64_t);
 void fs_scratch_address(uint64_t*);
 void fs_gather_elems(uint64_t, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint64_t);
@@ -337,6 +339,8 @@ static emu_function g_funcs[] = {
     {"fs_onesweep_any_k64", [](void** p) { fs_onesweep_any_k64(A0, D1); }},
     {"fs_first_k32", [](void** p) { fs_first_k32(A0); }},
     {"fs_first_k64", [](void** p) { fs_first_k64(A0); }},
+    {"fs_region_sample_k32", [](void** p) { fs_region_sample_k32(A0); }},
+    {"fs_region_sample_k64", [](void** p) { fs_region_sample_k64(A0); }},
     {"fs_iota", [](void** p) { fs_iota(*(uint32_t**)p[0], *(uint64_t*)p[1]); }},
     {"fs_scratch_address", [](void** p) { fs_scratch_address(*(uint64_t**)p[0]); }},
     {"fs_gather_elems", [](void** p) {

@@ -31,7 +31,7 @@ def use_emulator(flavor):
     forge_sort._lib = None
 
 
-def keys_for(kind, n, dist, seed):
+def keys_for(kind, n, dist, seed, tile=None):
     g = np.random.Generator(np.random.PCG64(seed))
     wide = BITS[kind] == np.uint64
     if dist == "uniform":
@@ -52,9 +52,17 @@ def keys_for(kind, n, dist, seed):
         b = (g.integers(0, 256, size=n, dtype=BITS[kind]) << BITS[kind](8)).astype(BITS[kind])
     elif dist == "skew0":
         # lowest byte 3 or 200, the rest uniform: the fused first pass's
-        # regions of those two digit values overflow
+        # sampled region sizes give those two digit values all the room
         b = g.integers(0, 1 << (64 if wide else 32), size=n, dtype=BITS[kind], endpoint=False)
         b = (b & ~BITS[kind](0xFF)) | np.where(g.integers(0, 2, size=n) == 0, 3, 200).astype(BITS[kind])
+    elif dist == "grp0":
+        # lowest byte 3 in the tiles of the fused pass's region group 0
+        # ((tile / 8) % 8 == 0, tiles of `tile` keys), uniform elsewhere: the
+        # input-wide sample underrates digit 3 for that group, whose region
+        # of it overflows once other groups hold tiles
+        b = g.integers(0, 1 << (64 if wide else 32), size=n, dtype=BITS[kind], endpoint=False)
+        in0 = (np.arange(n) // tile // 8) % 8 == 0
+        b[in0] = (b[in0] & ~BITS[kind](0xFF)) | BITS[kind](3)
     elif dist == "zipf":
         # a dominant bin: Zipf(1.1) ranks below 2^20 (most keys small, digit 1
         # and 2 mostly zero), as in the pairs benchmark config
@@ -226,7 +234,7 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
     """A keys-only sort, exact, that began the way the case names
     (fs_sorter_first_pass), with the fused first pass at every size, or
     ("nofused") never."""
-    keys = keys_for(kind, n, dist, seed)
+    keys = keys_for(kind, n, dist, seed, tile=sorter.tile_config()["k64" if BITS[kind] == np.uint64 else "k32"])
     sorter.set_test_option(forge_sort.TEST_FUSED,
                            forge_sort.FUSED_NEVER if op == "nofused" else forge_sort.FUSED_ALWAYS)
     try:

@@ -90,15 +90,18 @@ FUSED_SMALL = [
     # regions copied back); two digits vary
     "fused:u32:9000:uniform:1", "fused:f32:20000:uniform:2", "fused:u32:1025:uniform:3",
     "fused:i32:2:uniform:4", "fused:i32:5000:byte0:5", "fused:u32:3000:low12:6",
-    # a region overflows (skewed lowest byte; lowest byte constant), or every
+    # skewed lowest byte, lowest byte constant: regions sized by the sample
+    "fused:u32:9000:skew0:7", "fused:f32:6000:byte1:8",
+    # a region overflows (digit 3 crowded into one region group), or every
     # digit is constant: stable passes over the caller's keys
-    "fusedover:u32:9000:skew0:7", "fusedover:f32:6000:byte1:8", "fusedover:u32:50:same:9",
+    "fusedover:u32:30000:grp0:19", "fusedover:f32:30001:grp0:20", "fusedover:u32:50:same:9",
     "fusedover:u32:9000:same:10",
     # the testing hook: the histogram read instead
     "nofused:u32:9000:uniform:11", "nofused:i32:4099:byte0:12",
     # 64-bit keys: seven upper digits counted, regions of 8-byte keys
     "fused:u64:9000:uniform:13", "fused:f64:5001:uniform:14", "fused:i64:3000:byte0:15",
-    "fusedover:u64:6000:skew0:16", "fusedover:f64:40:same:17", "nofused:u64:3000:uniform:18",
+    "fused:u64:6000:skew0:16", "fusedover:u64:20000:grp0:21", "fusedover:f64:40:same:17",
+    "nofused:u64:3000:uniform:18",
 ]
 
 
@@ -109,13 +112,13 @@ def test_emulated_fused_first_pass(emulator):
     it in the groups build."""
     run_cases("small", FUSED_SMALL)
     run_cases("prod", ["fused:u32:100000:uniform:1", "fused:f32:17665:uniform:2", "fused:u32:40000:byte0:3",
-                       "fusedover:u32:40000:skew0:4", "nofused:u32:40000:uniform:5", "fused:u64:30000:uniform:6",
-                       "fused:i64:7681:uniform:7"])
-    run_cases("groups", ["fused:u32:70000:uniform:1", "fusedover:i32:30000:skew0:2"], env={"EMU_CUS": "8"})
+                       "fusedover:u32:450000:grp0:4", "nofused:u32:40000:uniform:5", "fused:u64:30000:uniform:6",
+                       "fused:i64:7681:uniform:7", "fused:u32:40000:skew0:8"])
+    run_cases("groups", ["fused:u32:70000:uniform:1", "fusedover:i32:30000:grp0:2"], env={"EMU_CUS": "8"})
     # regions larger than tiles: one- and two-region tile descriptors (and
     # more-region tiles where a region holds fewer keys than a tile)
     run_cases("regions", ["fused:u32:60000:uniform:1", "fused:f32:150001:uniform:2", "fused:i32:50000:byte0:3",
-                          "fused:u32:40000:low12:4", "fusedover:u32:60000:skew0:5", "noalloc:u32:60000:uniform:6",
+                          "fused:u32:40000:low12:4", "fused:u32:60000:skew0:5", "noalloc:u32:60000:uniform:6",
                           "sort:u64:9000:uniform:7", "pairs:u32:9000:uniform:8", "fused:u64:20000:uniform:9",
                           "fused:f64:9000:low12:10"], env={"EMU_TEST_FUSED": "2"})
 
@@ -209,7 +212,7 @@ def test_emulated_sanitizers(emulator):
     # ASan reports its own faults: the emulator's guard-page handler stays off
     run_cases("san", ["sort:u32:5000:uniform:1", "sort:f32:3001:uniform:3", "argsort:i32:2000:few:7",
                       "pairs:f64:2500:uniform:12", "sort:u32:5000:byte0:31", "sort:u32:9000:zipf:28",
-                      "gather:u32:3000:uniform:26", "fused:u32:9000:uniform:40", "fusedover:u32:9000:skew0:41",
+                      "gather:u32:3000:uniform:26", "fused:u32:9000:uniform:40", "fusedover:u32:30000:grp0:41",
                       "fused:u32:5000:byte0:42"],
               timeout=600, env={"LD_PRELOAD": libasan, "EMU_NO_SEGV_HANDLER": "1", "EMU_CUS": "4", "EMU_TEST_FUSED": "2",
                                 "ASAN_OPTIONS": "detect_leaks=0:detect_stack_use_after_return=0"})

@@ -108,7 +108,7 @@ def test_golden(sorter, case):
 
 # ---- edge cases and sizes ------------------------------------------------------
 
-def make_keys(kind, n, dist, seed):
+def make_keys(kind, n, dist, seed, tile=None):
     g = np.random.Generator(np.random.PCG64(seed))
     wide = BITS[kind] == np.uint64
     hi = 1 << (64 if wide else 32)
@@ -133,6 +133,10 @@ def make_keys(kind, n, dist, seed):
     elif dist == "skew0":       # lowest byte 3 or 200, the rest uniform
         b = g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False)
         b = (b & ~BITS[kind](0xFF)) | np.where(g.integers(0, 2, size=n) == 0, 3, 200).astype(BITS[kind])
+    elif dist == "grp0":        # lowest byte 3 in the tiles ((tile / 8) % 8 == 0) of region group 0
+        b = g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False)
+        in0 = (np.arange(n) // tile // 8) % 8 == 0
+        b[in0] = (b[in0] & ~BITS[kind](0xFF)) | BITS[kind](3)
     else:
         raise ValueError(dist)
     keys = b.view(NP[kind])
@@ -297,9 +301,12 @@ FUSED_CASES = [
     # its regions feed the next pass: every digit varies; only digit 0 (the
     # regions copied back); digits 0 and 1
     (1_000_003, "uniform", 1), (16_777_216, "uniform", 1), (300_007, "byte0", 1), (2_000_000, "lowbits", 1),
-    # a region overflows (skewed lowest byte; lowest byte constant) or every
-    # digit is constant: the standard schedule over the caller's keys
-    (1_000_000, "skew0", 2), (500_000, "byte1", 2), (100_003, "same", 2),
+    # regions sized by the sampled lowest byte: two values; one value
+    (1_000_000, "skew0", 1), (500_000, "byte1", 1),
+    # a region overflows (digit 3 crowded into region group 0, which the
+    # input-wide sample underrates) or every digit is constant: the standard
+    # schedule over the caller's keys
+    (2_000_000, "grp0", 2), (100_003, "same", 2),
 ]
 
 
@@ -311,7 +318,8 @@ def test_fused_first_pass(sorter, kind, n, dist, expect):
     forced at every size: exact against the oracle on both of its schedules,
     through the slice and buffer APIs; the histogram read gives the same keys."""
     from forge_sort import FIRST_HISTOGRAM, FUSED_ALWAYS, FUSED_BY_SIZE, FUSED_NEVER, TEST_FUSED
-    keys = make_keys(kind, n, dist, seed=900 + n % 97)
+    keys = make_keys(kind, n, dist, seed=900 + n % 97,
+                     tile=sorter.tile_config()[TILE_VARIANT[("sort", BITS[kind] == np.uint64)]])
     sorter.set_test_option(TEST_FUSED, FUSED_ALWAYS)
     try:
         check_sort(sorter, kind, keys)
@@ -326,7 +334,10 @@ def test_fused_first_pass(sorter, kind, n, dist, expect):
         sorter.set_test_option(TEST_FUSED, FUSED_NEVER)
         check_sort(sorter, kind, keys)
         assert sorter.first_pass() == FIRST_HISTOGRAM
-        assert sorter.last_pass_info() == (passes, mask)
+        # the same digits run, but a fused pass that used its regions counts
+        # as digit 0's pass even where digit 0 is constant
+        hp, hm = sorter.last_pass_info()
+        assert hm == (mask & ~1 if expect == 1 and dist == "byte1" else mask) and hp == bin(hm).count("1")
     finally:
         sorter.set_test_option(TEST_FUSED, FUSED_BY_SIZE)
 
@@ -700,9 +711,10 @@ def test_graph_capture_replays(hip_stream, op):
         s.encode(code, "u32", kb.device_ptr(), vb.device_ptr(), n, stream=hip_stream)
         assert hip.hipStreamEndCapture(st, ctypes.byref(graph)) == 0
         assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
-        dists = ["uniform", "few", "lowbits", "byte1"] if pairs else ["uniform", "skew0", "same", "byte0", "uniform"]
+        dists = ["uniform", "few", "lowbits", "byte1"] if pairs else ["uniform", "skew0", "grp0", "same", "byte0",
+                                                                       "uniform"]
         for r, dist in enumerate(dists):
-            keys = make_keys("u32", n, dist, seed=910 + r)
+            keys = make_keys("u32", n, dist, seed=910 + r, tile=s.tile_config()["k32"])
             vals = g.integers(0, 1 << 32, size=n, dtype=np.uint32)
             kb.copy_from_slice(keys)
             vb.copy_from_slice(vals)
