@@ -52,7 +52,7 @@ METRIC = "Mkeys/s (u32 256M, 1 MI355X) and % of HBM-bandwidth roofline vs host C
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 PASS_BYTES_PER_KEY = 8         # one read + one write of a u32 key per digit pass
 SORT_BYTES_PER_KEY = 36        # k + k*2*k for k = 4 (histogram read + 4 passes)
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "onesweep_k32_u32_256M_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fs_onesweep_k32_u32_256M_traffic.json")
 
 
 # name -> (op, key type, n, data description, BASELINE.json config)
