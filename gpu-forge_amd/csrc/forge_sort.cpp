@@ -447,6 +447,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
 #ifdef FS_FAULT_INJECTION
     a.fault = s->fault;
     if (s->fault == FS_FAULT_BAD_DIGITS) a.digits = 5u;
+    if (s->fault == FS_FAULT_SMALL_S1) a.s1_keys /= 2u;
 #endif
 
     void* args1[] = {&a};
@@ -793,7 +794,7 @@ fs_status fs_sorter_set_test_option(fs_sorter* s, fs_test_option opt, uint64_t v
             return FS_OK;
         case FS_TEST_INJECT_FAULT:
 #ifdef FS_FAULT_INJECTION
-            if (value > FS_FAULT_STALL_TILE) return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown fault %llu",
+            if (value > FS_FAULT_SMALL_S1) return set_err(s, FS_ERR_INVALID_ARGUMENT, "unknown fault %llu",
                                                            (unsigned long long)value);
             s->fault = (uint32_t)value;
             return FS_OK;

@@ -229,6 +229,8 @@
 #define FS_FAULT_BAD_BUFFER 2u     // schedule names an unknown buffer for the first pass -> BAD_PLAN
 #define FS_FAULT_EXTRA_BLOCK 3u    // first digit pass launched with one block too many -> BAD_TILE
 #define FS_FAULT_STALL_TILE 4u     // tile 1 of the first pass never publishes -> LOOKBACK_TIMEOUT
+#define FS_FAULT_SMALL_S1 5u       // the region sample's S1 budget halved: its layout does not fit and
+                                   // the regions split the budget evenly (no error; the sort stays exact)
 
 // Scratch of the entry point that allocates nothing (fs_encode_no_alloc): a
 // file-scope static device array of FS_NA_SCRATCH_BYTES in the code object,

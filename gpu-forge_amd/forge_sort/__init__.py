@@ -40,7 +40,7 @@ FUSED_BY_SIZE, FUSED_NEVER, FUSED_ALWAYS = 0, 1, 2       # TEST_FUSED values
 FUSED_MIN_KEYS = 1 << 25                                 # FS_FUSED_MIN_KEYS
 # fs_sorter_first_pass: how the last sort began
 FIRST_HISTOGRAM, FIRST_FUSED, FIRST_FUSED_OVERFLOW = 0, 1, 2
-FAULT_NONE, FAULT_BAD_DIGITS, FAULT_BAD_BUFFER, FAULT_EXTRA_BLOCK, FAULT_STALL_TILE = 0, 1, 2, 3, 4
+FAULT_NONE, FAULT_BAD_DIGITS, FAULT_BAD_BUFFER, FAULT_EXTRA_BLOCK, FAULT_STALL_TILE, FAULT_SMALL_S1 = 0, 1, 2, 3, 4, 5
 
 FS_OK = 0
 FS_ERR_DEVICE_NOT_FOUND = 1

@@ -144,6 +144,30 @@ def check_fault(sorter, op, kind, keys):
     return sorted_ok(sorter, kind, keys)
 
 
+def check_small_s1(sorter, kind, keys):
+    """A fused sort whose region sample gets half the S1 budget it was sized
+    for: the sample refuses its layout and splits the budget evenly; the
+    regions then hold the keys (small inputs, where the per-region margin
+    dominates the budget) or overflow into the stable passes.  Exact either
+    way, and exact again without the fault."""
+    sorter.set_test_option(forge_sort.TEST_INJECT_FAULT, forge_sort.FAULT_SMALL_S1)
+    sorter.set_test_option(forge_sort.TEST_FUSED, forge_sort.FUSED_ALWAYS)
+    try:
+        ok = sorted_ok(sorter, kind, keys)
+        first = sorter.first_pass()
+    finally:
+        sorter.set_test_option(forge_sort.TEST_INJECT_FAULT, forge_sort.FAULT_NONE)
+    try:
+        ok = ok and sorted_ok(sorter, kind, keys) and sorter.first_pass() == forge_sort.FIRST_FUSED
+    finally:
+        sorter.set_test_option(forge_sort.TEST_FUSED, FUSED_MODE)
+    if first not in (forge_sort.FIRST_FUSED, forge_sort.FIRST_FUSED_OVERFLOW):
+        print(f"  first pass {first} with half the budget, expected the fused pass", flush=True)
+        ok = False
+    print(f"  first pass {first} with half the budget", flush=True)
+    return ok
+
+
 def check_timeout_or_exact(sorter, kind, keys):
     """A digit pass whose XCD queue is held back (EMU_HOLD_QUEUE): either the
     held tiles arrive within the spin bound and the sort is exact, or the
@@ -260,9 +284,11 @@ def check(sorter, op, kind, n, dist, seed):
         ok = check_no_alloc(sorter, kind, n, dist, seed)
         print(f"{'PASS' if ok else 'FAIL'} {op} {kind} n={n}", flush=True)
         return ok
-    if op in FAULTS or op in ("hold", "capture"):
+    if op in FAULTS or op in ("hold", "capture", "small_s1"):
         if op == "capture":
             ok = check_capture(sorter, kind, n, seed)
+        elif op == "small_s1":
+            ok = check_small_s1(sorter, kind, keys_for(kind, n, dist, seed))
         elif op == "hold":
             ok = check_timeout_or_exact(sorter, kind, keys_for(kind, n, dist, seed))
         else:

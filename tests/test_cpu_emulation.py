@@ -169,7 +169,9 @@ def test_emulated_device_error_guards(emulator):
     its own message, and the next sort is exact again: a digit count that does
     not match the key width, a schedule naming an unknown buffer, a digit-pass
     block beyond the tile grid, and a tile that never publishes (its
-    successors' look-back waits end at the build's tiny spin bound)."""
+    successors' look-back waits end at the build's tiny spin bound).  Also the
+    region sample's safety net, which raises no error: a region layout larger
+    than the S1 budget is replaced by an even split and the sort stays exact."""
     run_cases("faults", ["fault_digits:u32:5000:uniform:1", "fault_digits:u64:3000:uniform:2",
                          "fault_buffer:u32:5000:uniform:3", "fault_buffer:i64:3000:uniform:4",
                          "fault_tile:u32:5000:uniform:5", "fault_tile:f64:3000:uniform:6",
@@ -179,6 +181,9 @@ def test_emulated_device_error_guards(emulator):
     run_cases("faults", ["fault_digits:u32:5000:uniform:1", "fault_buffer:f32:5000:uniform:3",
                          "fault_tile:u32:5000:uniform:5", "fault_stall:i32:9000:uniform:7"],
               env={"EMU_CUS": "8", "EMU_TEST_FUSED": "2"})
+    # the region sample's safety net: a layout that would not fit the S1 the
+    # host sized is replaced by an even split (the sort stays exact)
+    run_cases("faults", ["small_s1:u32:30000:uniform:9", "small_s1:u64:20000:skew0:10"], env={"EMU_CUS": "8"})
 
 
 def test_emulated_held_xcd_queue(emulator):
