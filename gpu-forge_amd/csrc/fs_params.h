@@ -127,6 +127,12 @@
 #define FS_PASS_FIRST 1u   // apply the forward key transform on load; argsort: generate indices
 #define FS_PASS_LAST 2u    // apply the inverse transform on store; argsort: do not store keys
 #define FS_PASS_REGIONED 4u  // the source is the fused first pass's region layout (see below)
+#define FS_PASS_SKEWED 8u    // a bin of the digit holds more than 1/FS_SKEW_SHARE of the keys: the
+                             // pass's tile histogram uses replicated counters
+#ifndef FS_SKEW_SHARE
+#define FS_SKEW_SHARE 64u
+#endif
+#define FS_SKEW_BIT (1u << 16)  // schedule steps: bit 16 + j of their constant mask marks digit j skewed
 
 // Operation.
 #define FSK_OP_KEYS 0u
