@@ -195,7 +195,9 @@
 // the S1 index of position p is p + (p < y ? x : z) (y: first position of the
 // second region, or 0xFFFFFFFF); with FS_TILE_MULTI, x is the region of the
 // tile's last key and indices come from the region start table.
+// FS_TILE_ONE_DIGIT: every region of the tile holds the same digit-0 value.
 #define FS_TILE_MULTI 0x80000000u
+#define FS_TILE_ONE_DIGIT 0x40000000u
 #define FS_TILE_DESC_WORDS 4
 #define FS_HIST_WORDS (FS_HIST_SLOTS * FS_MAX_DIGITS * FS_RADIX)
 
