@@ -187,8 +187,10 @@
                                     (unsigned long long)FS_REGIONS * 65ull)
 // Histogram table: FS_HIST_SLOTS copies of [FS_MAX_DIGITS][FS_RADIX]; the
 // fused pass's tiles fold their counts into copy (tile % FS_HIST_SLOTS), so
-// that no counter takes more than num_tiles / FS_HIST_SLOTS atomics.
-#define FS_HIST_SLOTS 16
+// that no counter takes more than num_tiles / FS_HIST_SLOTS atomics.  The
+// schedule step, in the pass's last tile, reads and clears every copy: 1 to 8
+// copies measured alike, 16 slower (u64: +5% fused pass), 32 slower still.
+#define FS_HIST_SLOTS 4
 // Tile descriptor of the region layout, 4 words {x, y, z, w} per tile of the
 // pass after the fused one.  w = region k0 of the tile's first key, with
 // FS_TILE_MULTI set when the tile covers more than two regions.  Otherwise

@@ -165,7 +165,7 @@ fs_status fs_encode(fs_sorter *s, fs_op op, fs_key_type type, void *device_keys,
  * the device race, so issue them on one stream or order them.  fs_encode's
  * scratch is separate. */
 #define FS_NO_ALLOC_MAX_KEYS 1048576u
-#define FS_NO_ALLOC_SCRATCH_BYTES 25632768u   /* 24.4 MiB with the gfx950 tile geometry */
+#define FS_NO_ALLOC_SCRATCH_BYTES 25534464u   /* 24.4 MiB with the gfx950 tile geometry */
 fs_status fs_encode_no_alloc(fs_sorter *s, fs_op op, fs_key_type type, void *device_keys,
                              uint32_t *device_values, uint64_t n, void *hip_stream);
 
