@@ -111,6 +111,9 @@
 #ifndef FS_LB_GROUP
 #define FS_LB_GROUP 16
 #endif
+// Two groups per round trip measured 0.5% faster per u32 256M sort than 4
+// and 1 (with 8-item staging batches); a tile window of 4 entries against 3
+// (equal) and 6 (slower).
 #ifndef FS_LB_GWIN
 #define FS_LB_GWIN 2
 #endif
