@@ -29,7 +29,7 @@
 #define FS_K64_BLOCK 768
 #endif
 #ifndef FS_K64_ITEMS
-#define FS_K64_ITEMS 10
+#define FS_K64_ITEMS 11
 #endif
 #ifndef FS_K64V_BLOCK
 #define FS_K64V_BLOCK 768

@@ -71,8 +71,8 @@ PROD_CASES = [
     "pairs:u64:20000:uniform:4", "sort:i64:20000:low12:6", "pairs:u32:25000:few:7",
     "sort:f64:9000:uniform:8", "argsort:i32:13000:uniform:9",
     "pairs:u32:30000:zipf:10", "sort:u32:26000:few:11",
-    # one key past a tile of the u32 (768 x 23), u64 (768 x 10) and u32+values (768 x 18) variants
-    "sort:u32:17665:uniform:12", "sort:u64:7681:uniform:13", "pairs:u32:13825:uniform:14",
+    # one key past a tile of the u32 (768 x 23), u64 (768 x 11) and u32+values (768 x 18) variants
+    "sort:u32:17665:uniform:12", "sort:u64:8449:uniform:13", "pairs:u32:13825:uniform:14",
 ]
 
 
@@ -113,7 +113,7 @@ def test_emulated_fused_first_pass(emulator):
     run_cases("small", FUSED_SMALL)
     run_cases("prod", ["fused:u32:100000:uniform:1", "fused:f32:17665:uniform:2", "fused:u32:40000:byte0:3",
                        "fusedover:u32:450000:grp0:4", "nofused:u32:40000:uniform:5", "fused:u64:30000:uniform:6",
-                       "fused:i64:7681:uniform:7", "fused:u32:40000:skew0:8"])
+                       "fused:i64:8449:uniform:7", "fused:u32:40000:skew0:8"])
     run_cases("groups", ["fused:u32:70000:uniform:1", "fusedover:i32:30000:grp0:2"], env={"EMU_CUS": "8"})
     # regions larger than tiles: one- and two-region tile descriptors (and
     # more-region tiles where a region holds fewer keys than a tile)
