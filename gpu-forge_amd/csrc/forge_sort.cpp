@@ -41,10 +41,11 @@ const char* const kKernelNames[] = {
     "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
     "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
+    "fs_local_k32",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
-    K_SAMPLE32, K_SAMPLE64, K_COUNT
+    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_COUNT
 };
 
 }  // namespace
@@ -57,6 +58,8 @@ struct fs_sorter {
     hipFunction_t fn[K_COUNT] = {};
     uint32_t tile[4] = {};          // keys per tile of each digit-pass variant (FS_VAR_*)
     uint32_t block[4] = {};         // threads per block of each variant
+    uint32_t local_keys = 0;        // keys a block of the local sort holds (fs_local_k32)
+    uint32_t local_block = 0;       // its threads per block
     int num_cus = 256;
 
     DevBuf s1k, s2k, s1v, s2v, lb0, lb1, iok, iov, tilemap;
@@ -66,6 +69,7 @@ struct fs_sorter {
     uint32_t* rstart = nullptr;     // [FS_REGIONS + 1] region starts
     uint32_t* rtable = nullptr;     // [FS_RTABLE_WORDS] region bases, total and caps of the fused pass
     uint32_t* plan = nullptr;       // u32[FS_PLAN_WORDS] device-side schedule
+    uint32_t* segc = nullptr;       // u32[FS_SEGS] segment counters of the top-16 path
     uint32_t* status = nullptr;     // pinned host word written by kernels on device errors
     unsigned long long* stats = nullptr;   // device u64[FS_STAT_COUNT]
     bool stats_on = false;
@@ -83,10 +87,12 @@ struct fs_sorter {
     // Test options (fs_sorter_set_test_option); defaults give the product layout.
     bool force_wide = false;             // 64-bit look-back entries for any n
     uint32_t fused_mode = 0;             // FS_TEST_FUSED: 0 by size, 1 never, 2 always
+    uint32_t top16_mode = 0;             // FS_TEST_TOP16: 0 by size, 1 never, 2 always
     // the last sort's schedule (the sorter's, or the static scratch's) and
     // whether it began with the fused first pass
     uint32_t* last_plan = nullptr;
     bool last_fused = false;
+    bool last_top16 = false;
     uint32_t up_blocks_per_cu = 0;       // upsweep blocks per CU (0: by key width)
     uint32_t fault = FS_FAULT_NONE;      // injected fault (FS_FAULT_INJECTION builds only)
 
@@ -305,6 +311,28 @@ static bool fused_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
     return s->fused_mode == 2u || n >= FS_FUSED_MIN_KEYS;
 }
 
+// Keys-only u32/i32 sorts from FS_TOP16_MIN_KEYS keys take the top-16 path
+// (fused pass on digit 2, stable pass on digit 3, local sort of each
+// segment); it needs the fused pass's regions, hence the fused range.
+static bool top16_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
+    if (op != FS_OP_SORT || (t != FS_KEY_U32 && t != FS_KEY_I32) || s->top16_mode == 1u || n < 2) return false;
+    if (n > (1ull << 31) || s->fused_mode == 1u) return false;
+    if (FS_FUSED_S1_KEYS(fused_sub_keys(n, s->tile[FS_VAR_K32])) >= (1ull << 32)) return false;
+    return s->top16_mode == 2u || n >= FS_TOP16_MIN_KEYS;
+}
+
+// Bits that name a segment of the local sort: a uniform input's segment then
+// holds between a half and all of 2^floor(log2(block keys)) keys on average,
+// so that nearly every segment fits one block; at least the top byte, at
+// most the top 16 bits the two digit passes order.
+static uint32_t seg_bits_for(uint64_t n, uint32_t local_keys) {
+    uint32_t lg_n = 0, lg_c = 0;
+    while ((2ull << lg_n) <= n) ++lg_n;
+    while ((2ull << lg_c) <= local_keys) ++lg_c;
+    const int b = (int)lg_n - (int)lg_c;
+    return b < 8 ? 8u : b > 16 ? 16u : (uint32_t)b;
+}
+
 // Grows the scratch a sort of n keys needs (grow-only, like ensure_buffers*,
 // lib.rs:1120-1289): ping-pong buffers for keys (and values), and two
 // look-back arrays of tile entries followed by one 32-bit group entry per
@@ -315,7 +343,7 @@ static fs_status reserve(fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
     const uint32_t tile = s->tile[variant_of(op, t)];
     const uint64_t num_tiles = (n + tile - 1) / tile;
     fs_status r;
-    const bool fused = fused_path(s, op, t, n);
+    const bool fused = fused_path(s, op, t, n) || top16_path(s, op, t, n);
     if ((r = ensure(s, s->s1k, (fused ? FS_FUSED_S1_KEYS(fused_sub_keys(n, tile)) : n) * kb)) != FS_OK) return r;
     if ((r = ensure(s, s->s2k, n * kb)) != FS_OK) return r;
     if (fused && (r = ensure(s, s->tilemap, num_tiles * FS_TILE_DESC_WORDS * 4)) != FS_OK) return r;
@@ -332,7 +360,7 @@ static fs_status reserve(fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
 // Device addresses of the scratch a sort uses: the sorter's own grow-only
 // buffers, or the static array of fs_encode_no_alloc.
 struct ScratchSet {
-    uint64_t s1k, s2k, s1v, s2v, lb0, lb1, hist, binbase, plan, cursors, rstart, tilemap, rtable;
+    uint64_t s1k, s2k, s1v, s2v, lb0, lb1, hist, binbase, plan, cursors, rstart, tilemap, rtable, segc;
 };
 
 static ScratchSet sorter_scratch(const fs_sorter* s) {
@@ -342,7 +370,7 @@ static ScratchSet sorter_scratch(const fs_sorter* s) {
                       (uint64_t)(uintptr_t)s->hist, (uint64_t)(uintptr_t)s->binbase,
                       (uint64_t)(uintptr_t)s->plan, (uint64_t)(uintptr_t)s->cursors,
                       (uint64_t)(uintptr_t)s->rstart, (uint64_t)(uintptr_t)s->tilemap.p,
-                      (uint64_t)(uintptr_t)s->rtable};
+                      (uint64_t)(uintptr_t)s->rtable, (uint64_t)(uintptr_t)s->segc};
 }
 
 static ScratchSet static_scratch(const fs_sorter* s) {
@@ -350,7 +378,7 @@ static ScratchSet static_scratch(const fs_sorter* s) {
     return ScratchSet{p + FS_NA_OFF_S1K, p + FS_NA_OFF_S2K, p + FS_NA_OFF_S1V, p + FS_NA_OFF_S2V,
                       p + FS_NA_OFF_LB0, p + FS_NA_OFF_LB1, p + FS_NA_OFF_HIST, p + FS_NA_OFF_BINBASE,
                       p + FS_NA_OFF_PLAN, p + FS_NA_OFF_CURSORS, p + FS_NA_OFF_RSTART, p + FS_NA_OFF_TILEMAP,
-                      p + FS_NA_OFF_RTABLE};
+                      p + FS_NA_OFF_RTABLE, 0};   // (no top-16 path on the static scratch)
 }
 
 // no_alloc: the sort runs on the static scratch (fs_encode_no_alloc): nothing
@@ -399,8 +427,9 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     // the fused first pass, when its regions fit the scratch (the static
     // scratch's S1 holds FS_NA_MAX_KEYS 8-byte keys)
     const uint64_t sub_keys = fused_sub_keys(n, tile);
-    const bool fused = fused_path(s, op, t, n) &&
-                       (!no_alloc || FS_FUSED_S1_KEYS(sub_keys) * kb <= (uint64_t)FS_NA_MAX_KEYS * 8);
+    const bool top16 = !no_alloc && top16_path(s, op, t, n);
+    const bool fused = top16 || (fused_path(s, op, t, n) &&
+                                 (!no_alloc || FS_FUSED_S1_KEYS(sub_keys) * kb <= (uint64_t)FS_NA_MAX_KEYS * 8));
 
     FsArgs a;
     memset(&a, 0, sizeof a);
@@ -442,6 +471,9 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.fused = fused ? 1u : 0u;
     a.sub_keys = fused ? (uint32_t)sub_keys : 0u;
     a.s1_keys = fused ? (uint32_t)FS_FUSED_S1_KEYS(sub_keys) : 0u;
+    a.sdigit = top16 ? 2u : 0u;
+    a.segc = top16 ? sc.segc : 0u;
+    a.seg_bits = top16 ? seg_bits_for(n, s->local_keys) : 0u;
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 #ifdef FS_FAULT_INJECTION
@@ -451,6 +483,31 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
 #endif
 
     void* args1[] = {&a};
+    if (top16) {
+        // region sample (digit 2) -> fused pass (digit 2) -> its re-scatter
+        // launch (works only after an overflow) -> the stable pass on digit 3
+        // (launch slot 0) -> the local sort, one block per segment
+        if ((r = launch(s, K_SAMPLE32, 1, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK) return r;
+        unsigned grid = num_tiles;
+#ifdef FS_FAULT_INJECTION
+        if (s->fault == FS_FAULT_EXTRA_BLOCK) grid += 1u;
+#endif
+        for (uint32_t l = 0; l < 2; ++l) {
+            uint32_t which = l;
+            void* argsf[] = {&a, &which};
+            if ((r = launch(s, K_FIRST32, l ? num_tiles : grid, s->block[var], argsf, st, no_alloc)) != FS_OK) return r;
+        }
+        uint32_t slot = 0;
+        void* args2[] = {&a, &slot};
+        if ((r = launch(s, K_OS32, num_tiles, s->block[var], args2, st, no_alloc)) != FS_OK) return r;
+        if ((r = launch(s, K_LOCAL32, 1u << a.seg_bits, s->local_block, args1, st, no_alloc)) != FS_OK) return r;
+        s->last_stream = st;
+        s->pending = true;
+        s->last_plan = (uint32_t*)(uintptr_t)sc.plan;
+        s->last_fused = true;
+        s->last_top16 = true;
+        return FS_OK;
+    }
     if (fused) {
         if ((r = launch(s, key64(t) ? K_SAMPLE64 : K_SAMPLE32, 1, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK)
             return r;
@@ -458,7 +515,9 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
 #ifdef FS_FAULT_INJECTION
         if (s->fault == FS_FAULT_EXTRA_BLOCK) grid += 1u;
 #endif
-        if ((r = launch(s, key64(t) ? K_FIRST64 : K_FIRST32, grid, s->block[var], args1, st, no_alloc)) != FS_OK)
+        uint32_t first_launch = 0;
+        void* argsf[] = {&a, &first_launch};
+        if ((r = launch(s, key64(t) ? K_FIRST64 : K_FIRST32, grid, s->block[var], argsf, st, no_alloc)) != FS_OK)
             return r;
     } else {
         const unsigned up_grid = (unsigned)up_blocks;
@@ -481,6 +540,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     s->pending = true;
     s->last_plan = (uint32_t*)(uintptr_t)sc.plan;
     s->last_fused = fused;
+    s->last_top16 = false;
     return FS_OK;
 }
 
@@ -583,12 +643,21 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
         for (int i = 0; i < 4; ++i)
             if (s->tile[i] == 0 || s->block[i] < FS_RADIX)
                 return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object has an invalid tile geometry");
+        hipDeviceptr_t lp = nullptr;
+        size_t lsz = 0;
+        uint32_t lg[2] = {0, 0};
+        if (hipModuleGetGlobal(&lp, &lsz, s->module, "fs_kernel_local_geometry") != hipSuccess || lsz != 8 ||
+            hipMemcpyDtoH(lg, lp, 8) != hipSuccess || lg[0] == 0 || lg[1] < FS_RADIX)
+            return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object lacks a valid fs_kernel_local_geometry");
+        s->local_keys = lg[0];
+        s->local_block = lg[1];
     }
     const size_t tab = (size_t)FS_MAX_DIGITS * FS_RADIX * 4;
     if (hipMalloc(&s->hist, (size_t)FS_HIST_WORDS * 4) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||
         hipMalloc(&s->cursors, FS_REGIONS * 4) != hipSuccess || hipMalloc(&s->rstart, (FS_REGIONS + 1) * 4) != hipSuccess ||
         hipMalloc(&s->rtable, FS_RTABLE_WORDS * 4) != hipSuccess ||
         hipMalloc(&s->plan, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc(&s->segc, FS_SEGS * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc(&s->stats, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
         return create_failed(s, FS_ERR_OUT_OF_MEMORY, "device tables of the sorter");
@@ -644,6 +713,7 @@ void fs_sorter_free(fs_sorter* s) {
     if (s->rtable) (void)hipFree(s->rtable);
     if (s->binbase) (void)hipFree(s->binbase);
     if (s->plan) (void)hipFree(s->plan);
+    if (s->segc) (void)hipFree(s->segc);
     if (s->stats) (void)hipFree(s->stats);
     if (s->status) (void)hipHostFree(s->status);
     for (int b = 0; b < 2; ++b) {
@@ -786,6 +856,10 @@ fs_status fs_sorter_set_test_option(fs_sorter* s, fs_test_option opt, uint64_t v
         case FS_TEST_FUSED:
             if (value > 2) return set_err(s, FS_ERR_INVALID_ARGUMENT, "fused mode %llu > 2", (unsigned long long)value);
             s->fused_mode = (uint32_t)value;
+            return FS_OK;
+        case FS_TEST_TOP16:
+            if (value > 2) return set_err(s, FS_ERR_INVALID_ARGUMENT, "top-16 mode %llu > 2", (unsigned long long)value);
+            s->top16_mode = (uint32_t)value;
             return FS_OK;
         case FS_TEST_UPSWEEP_BLOCKS_PER_CU:
             if (value > 64) return set_err(s, FS_ERR_INVALID_ARGUMENT, "upsweep blocks per CU %llu > 64",
@@ -945,10 +1019,13 @@ fs_status fs_sorter_first_pass(fs_sorter* s, uint32_t* kind) {
     if (!s || !kind) return FS_ERR_INVALID_ARGUMENT;
     fs_status r = drain(s);
     if (r != FS_OK) return r;
-    uint32_t mask = 0;
-    HIP_TRY(s, hipMemcpy(&mask, (s->last_plan ? s->last_plan : s->plan) + FS_PLAN_MASK, sizeof mask,
-                         hipMemcpyDeviceToHost));
-    *kind = !s->last_fused ? 0u : (mask & FS_MASK_FUSED) ? 1u : 2u;
+    uint32_t w[FS_PLAN_WORDS];
+    HIP_TRY(s, hipMemcpy(w, s->last_plan ? s->last_plan : s->plan, sizeof w, hipMemcpyDeviceToHost));
+    const uint32_t mask = w[FS_PLAN_MASK];
+    if (s->last_top16 && (mask & FS_MASK_TOP16))
+        *kind = w[FS_PLAN_RESCATTER] ? 4u : 3u;
+    else
+        *kind = !s->last_fused ? 0u : (mask & FS_MASK_FUSED) ? 1u : 2u;
     return FS_OK;
 }
 

@@ -134,6 +134,8 @@
 #define FS_PASS_REGIONED 4u  // the source is the fused first pass's region layout (see below)
 #define FS_PASS_SKEWED 8u    // a bin of the digit holds more than 1/FS_SKEW_SHARE of the keys: the
                              // pass's tile histogram uses replicated counters
+#define FS_PASS_SEGCOUNT 16u // the pass (digit 3 of the top-16 path, reading keys in digit-2 order)
+                             // adds the keys of every top-16-bit segment to FsArgs.segc
 #ifndef FS_SKEW_SHARE
 #define FS_SKEW_SHARE 64u
 #endif
@@ -222,14 +224,42 @@
 #define FS_BUF_S2K 4u
 #define FS_BUF_S1V 5u
 #define FS_BUF_S2V 6u
-// per digit j: word 2j   = active | exec_index << 8 | flags << 16 | duty << 24
+// per digit-pass launch slot j (the launch's `slot` argument; in the LSD
+// schedules slot j sorts digit j):
+//              word 2j   = active | digit << 1 | exec_index << 8 | flags << 16 | duty << 24
 //              word 2j+1 = src_k | dst_k << 8 | src_v << 16 | dst_v << 24 (buffer ids)
 #define FS_PLAN_PASS_WORDS 2
 #define FS_PLAN_NPASSES (FS_MAX_DIGITS * FS_PLAN_PASS_WORDS)      // passes that run
 #define FS_PLAN_MASK (FS_PLAN_NPASSES + 1)                         // bit j: digit j sorted
-#define FS_MASK_FUSED (1u << 8)     // mask word: digit 0 sorted by the fused first pass's regions
+#define FS_MASK_FUSED (1u << 8)     // mask word: the fused first pass's regions were used
+#define FS_MASK_TOP16 (1u << 9)     // mask word: the top-16 path ran (digit passes on digits 2 and 3,
+                                    // then the local sort of each top-16-bit segment)
 #define FS_PLAN_TICKET (FS_PLAN_NPASSES + 2)                       // upsweep blocks finished (0 between sorts)
-#define FS_PLAN_WORDS (FS_PLAN_NPASSES + 3)
+// Local sort of the top-16 path (fs_local_*): word FS_PLAN_LOCAL = active | seg_bits << 8 |
+// flags << 16, word FS_PLAN_LOCAL + 1 = buffer ids as a pass's word 2j+1.
+#define FS_PLAN_LOCAL (FS_PLAN_NPASSES + 4)
+// 1: the fused pass's second launch re-scatters the keys into exact regions
+// (a region of its first launch overflowed); 0: that launch does nothing
+#define FS_PLAN_RESCATTER (FS_PLAN_NPASSES + 6)
+#define FS_PLAN_WORDS (FS_PLAN_NPASSES + 8)
+
+// Top-16 path of keys-only 32-bit sorts (from FS_TOP16_MIN_KEYS keys): the
+// fused first pass scatters by digit 2 (FsArgs.sdigit) into its regions, a
+// stable pass on digit 3 reads the regions in digit-2 order - so its output is
+// ordered by the top 16 bits - and counts the keys of every top-16-bit value
+// (FS_SEGS counters), and the local sort (fs_local_*) sorts each segment of
+// keys sharing their top seg_bits bits, in LDS, by the bits below: one block
+// per segment, one read and one write of every key.  A segment larger than a
+// block holds is sorted by that block through scratch, a digit at a time.
+// seg_bits is chosen on the host so that a segment holds about
+// 2^FS_LOCAL_LOG2 keys of a uniform input.
+#define FS_SEGS 65536u
+#ifndef FS_L32_BLOCK
+#define FS_L32_BLOCK 256
+#endif
+#ifndef FS_L32_ITEMS
+#define FS_L32_ITEMS 18
+#endif
 
 // Error bits additionally reported through the status word.
 #define FS_DEVERR_BAD_TILE 2u        // a digit pass block mapped to a tile >= num_tiles
@@ -310,6 +340,9 @@ typedef struct FsArgs {
     uint32_t sub_keys;          // keys of the fullest region group (fused path), else 0
     uint32_t fused;             // 1: the sort starts with the fused first pass (keys-only)
     uint32_t s1_keys;           // keys S1 holds (fused path: the regions' budget), else 0
+    uint32_t sdigit;            // digit the fused pass scatters by (0; 2 on the top-16 path)
+    uint64_t segc;              // u32[FS_SEGS] keys per top-16-bit value (top-16 path; zero before its digit-3 pass)
+    uint32_t seg_bits;          // top-16 path: bits that name a segment of the local sort (8..16), else 0
     uint32_t reserved0;
 } FsArgs;
 

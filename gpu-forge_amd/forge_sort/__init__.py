@@ -35,11 +35,13 @@ KEY_SIZE = {"u32": 4, "i32": 4, "f32": 4, "u64": 8, "i64": 8, "f64": 8}   # Sort
 OP_SORT, OP_ARGSORT, OP_PAIRS = 0, 1, 2
 NO_ALLOC_MAX_KEYS = 1 << 20          # FS_NO_ALLOC_MAX_KEYS
 # fs_test_option and the FS_FAULT_* codes (include/forge_sort.h, csrc/fs_params.h)
-TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT, TEST_FUSED = 0, 1, 2, 3
+TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT, TEST_FUSED, TEST_TOP16 = 0, 1, 2, 3, 4
 FUSED_BY_SIZE, FUSED_NEVER, FUSED_ALWAYS = 0, 1, 2       # TEST_FUSED values
+TOP16_BY_SIZE, TOP16_NEVER, TOP16_ALWAYS = 0, 1, 2       # TEST_TOP16 values
 FUSED_MIN_KEYS = 1 << 25                                 # FS_FUSED_MIN_KEYS
+TOP16_MIN_KEYS = 1 << 25                                 # FS_TOP16_MIN_KEYS
 # fs_sorter_first_pass: how the last sort began
-FIRST_HISTOGRAM, FIRST_FUSED, FIRST_FUSED_OVERFLOW = 0, 1, 2
+FIRST_HISTOGRAM, FIRST_FUSED, FIRST_FUSED_OVERFLOW, FIRST_TOP16, FIRST_TOP16_RESCATTER = 0, 1, 2, 3, 4
 FAULT_NONE, FAULT_BAD_DIGITS, FAULT_BAD_BUFFER, FAULT_EXTRA_BLOCK, FAULT_STALL_TILE, FAULT_SMALL_S1 = 0, 1, 2, 3, 4, 5
 
 FS_OK = 0
@@ -384,15 +386,17 @@ class GpuSorter:
 
     def set_test_option(self, option, value):
         """Testing hooks (TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU,
-        TEST_INJECT_FAULT, TEST_FUSED): reach layouts the product uses only
+        TEST_INJECT_FAULT, TEST_FUSED, TEST_TOP16): reach layouts the product uses only
         at sizes too large for a test, choose the first pass, or inject a
         device-side fault (emulator builds)."""
         self._check(_load().fs_sorter_set_test_option(self._h, option, value))
 
     def first_pass(self):
         """How the last sort began: FIRST_HISTOGRAM, FIRST_FUSED (the fused
-        first pass, regions used) or FIRST_FUSED_OVERFLOW (a region overflowed;
-        stable passes over the caller's keys followed)."""
+        first pass, regions used), FIRST_FUSED_OVERFLOW (a region overflowed;
+        stable passes over the caller's keys followed), FIRST_TOP16 (the top-16
+        path) or FIRST_TOP16_RESCATTER (the top-16 path after a region
+        overflowed, its keys re-scattered into exact regions)."""
         k = ctypes.c_uint32()
         self._check(_load().fs_sorter_first_pass(self._h, ctypes.byref(k)))
         return k.value

@@ -222,9 +222,12 @@ typedef enum fs_test_option {
     FS_TEST_WIDE_LOOKBACK = 0,          /* value != 0: 64-bit look-back entries for any n */
     FS_TEST_UPSWEEP_BLOCKS_PER_CU = 1,  /* histogram blocks per CU, 1..64 (0 = by key width) */
     FS_TEST_INJECT_FAULT = 2,           /* FS_FAULT_* (fault-injection builds only) */
-    FS_TEST_FUSED = 3                   /* keys-only sorts begin with the fused first pass:
+    FS_TEST_FUSED = 3,                  /* keys-only sorts begin with the fused first pass:
                                            0 = from FS_FUSED_MIN_KEYS keys on (the default),
                                            1 = never, 2 = at every size */
+    FS_TEST_TOP16 = 4                   /* keys-only u32/i32 sorts take the top-16 path:
+                                           0 = from FS_TOP16_MIN_KEYS keys on (the default),
+                                           1 = never, 2 = at every size of at least 2 keys */
 } fs_test_option;
 fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t value);
 
@@ -234,11 +237,23 @@ fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t v
  * (measured for u32 and u64 keys). */
 #define FS_FUSED_MIN_KEYS 33554432u
 
+/* Keys-only u32 and i32 sorts from this many keys on (up to 2^31) take the
+ * top-16 path: the fused first pass on the second-highest byte, one stable
+ * pass on the highest byte, then a local sort of every segment of keys that
+ * share their top bits, in LDS - three reads and writes of the keys instead of
+ * four.  f32 keys keep the LSD passes (their exponent bytes make segments
+ * too large for one block). */
+#define FS_TOP16_MIN_KEYS 33554432u
+
 /* How the last completed sort began: 0 = the histogram read (argsort, pairs,
  * and keys-only sorts outside the fused range), 1 = the fused first pass of a
  * keys-only sort, its regions read by the next pass,
  * 2 = the fused first pass, then stable passes over the caller's keys (a
- * region overflowed on a skewed lowest byte, or every digit is constant). */
+ * region overflowed on a skewed lowest byte, or every digit is constant),
+ * 3 = the top-16 path (fused pass on the second-highest byte, its regions
+ * read by the pass on the highest byte, then the local sort),
+ * 4 = the top-16 path after a region of its fused pass overflowed (the keys
+ * re-scattered into exact regions by a second launch of the fused pass). */
 fs_status fs_sorter_first_pass(fs_sorter *s, uint32_t *kind);
 
 /* ---- GpuGather (forge-runtime/src/gather.rs:26-173) --------------------------

@@ -310,8 +310,9 @@ void fs_onesweep_k64(FsArgs, uint32_t);
 void fs_onesweep_k64_v(FsArgs, uint32_t);
 void fs_onesweep_any_k32(FsArgs, uint32_t);
 void fs_onesweep_any_k64(FsArgs, uint32_t);
-void fs_first_k32(FsArgs);
-void fs_first_k64(FsArgs);
+void fs_first_k32(FsArgs, uint32_t);
+void fs_first_k64(FsArgs, uint32_t);
+void fs_local_k32(FsArgs);
 void fs_region_sample_k32(FsArgs);
 void fs_region_sample_k64(FsArgs);
 void fs_iota(uint32_t*, uint64_t);
@@ -319,6 +320,7 @@ void fs_scratch_address(uint64_t*);
 void fs_gather_elems(uint64_t, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint64_t);
 extern uint32_t fs_kernel_tile_keys[4];
 extern uint32_t fs_kernel_block_threads[4];
+extern uint32_t fs_kernel_local_geometry[2];
 }
 
 struct emu_function {
@@ -337,8 +339,9 @@ static emu_function g_funcs[] = {
     {"fs_onesweep_k64_v", [](void** p) { fs_onesweep_k64_v(A0, D1); }},
     {"fs_onesweep_any_k32", [](void** p) { fs_onesweep_any_k32(A0, D1); }},
     {"fs_onesweep_any_k64", [](void** p) { fs_onesweep_any_k64(A0, D1); }},
-    {"fs_first_k32", [](void** p) { fs_first_k32(A0); }},
-    {"fs_first_k64", [](void** p) { fs_first_k64(A0); }},
+    {"fs_first_k32", [](void** p) { fs_first_k32(A0, D1); }},
+    {"fs_first_k64", [](void** p) { fs_first_k64(A0, D1); }},
+    {"fs_local_k32", [](void** p) { fs_local_k32(A0); }},
     {"fs_region_sample_k32", [](void** p) { fs_region_sample_k32(A0); }},
     {"fs_region_sample_k64", [](void** p) { fs_region_sample_k64(A0); }},
     {"fs_iota", [](void** p) { fs_iota(*(uint32_t**)p[0], *(uint64_t*)p[1]); }},
@@ -479,6 +482,7 @@ hipError_t hipModuleGetFunction(hipFunction_t* f, hipModule_t, const char* name)
 hipError_t hipModuleGetGlobal(hipDeviceptr_t* p, size_t* sz, hipModule_t, const char* name) {
     if (!strcmp(name, "fs_kernel_tile_keys")) { *p = fs_kernel_tile_keys; *sz = sizeof fs_kernel_tile_keys; return hipSuccess; }
     if (!strcmp(name, "fs_kernel_block_threads")) { *p = fs_kernel_block_threads; *sz = sizeof fs_kernel_block_threads; return hipSuccess; }
+    if (!strcmp(name, "fs_kernel_local_geometry")) { *p = fs_kernel_local_geometry; *sz = sizeof fs_kernel_local_geometry; return hipSuccess; }
     return hipErrorNotFound;
 }
 hipError_t hipModuleLaunchKernel(hipFunction_t f, unsigned gx, unsigned, unsigned, unsigned bx, unsigned,

@@ -63,6 +63,17 @@ def keys_for(kind, n, dist, seed, tile=None):
         b = g.integers(0, 1 << (64 if wide else 32), size=n, dtype=BITS[kind], endpoint=False)
         in0 = (np.arange(n) // tile // 8) % 8 == 0
         b[in0] = (b[in0] & ~BITS[kind](0xFF)) | BITS[kind](3)
+    elif dist == "grp2":
+        # byte 2 is 3 in the tiles of region group 0 (as grp0, for the top-16
+        # path's fused pass, which scatters by byte 2)
+        b = g.integers(0, 1 << (64 if wide else 32), size=n, dtype=BITS[kind], endpoint=False)
+        in0 = (np.arange(n) // tile // 8) % 8 == 0
+        b[in0] = (b[in0] & ~BITS[kind](0xFF0000)) | BITS[kind](0x30000)
+    elif dist == "top8":
+        # the top byte only two values: segments of the local sort far larger
+        # than a block holds
+        b = g.integers(0, 1 << 24, size=n, dtype=BITS[kind])
+        b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](24)
     elif dist == "zipf":
         # a dominant bin: Zipf(1.1) ranks below 2^20 (most keys small, digit 1
         # and 2 mostly zero), as in the pairs benchmark config
@@ -250,8 +261,12 @@ def check_no_alloc(sorter, kind, n, dist, seed):
 # the fused first pass of keys-only sorts: by size (the default), or
 # forced on for every case of a run (EMU_TEST_FUSED=2)
 FUSED_MODE = int(os.environ.get("EMU_TEST_FUSED", "0"))
+# the top-16 path of keys-only u32/i32 sorts: by size (the default), or
+# forced on (EMU_TEST_TOP16=2)
+TOP16_MODE = int(os.environ.get("EMU_TEST_TOP16", "0"))
 FIRST_PASS = {"fused": forge_sort.FIRST_FUSED, "fusedover": forge_sort.FIRST_FUSED_OVERFLOW,
-              "nofused": forge_sort.FIRST_HISTOGRAM}
+              "nofused": forge_sort.FIRST_HISTOGRAM, "top16": forge_sort.FIRST_TOP16,
+              "top16over": forge_sort.FIRST_TOP16_RESCATTER}
 
 
 def check_first_pass(sorter, op, kind, n, dist, seed):
@@ -259,16 +274,22 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
     (fs_sorter_first_pass), with the fused first pass at every size, or
     ("nofused") never."""
     keys = keys_for(kind, n, dist, seed, tile=sorter.tile_config()["k64" if BITS[kind] == np.uint64 else "k32"])
+    top16 = op.startswith("top16")
     sorter.set_test_option(forge_sort.TEST_FUSED,
                            forge_sort.FUSED_NEVER if op == "nofused" else forge_sort.FUSED_ALWAYS)
+    sorter.set_test_option(forge_sort.TEST_TOP16, forge_sort.TOP16_ALWAYS if top16 else forge_sort.TOP16_NEVER)
     try:
         ok = sorted_ok(sorter, kind, keys)
         first = sorter.first_pass()
         passes, mask = sorter.last_pass_info()
     finally:
         sorter.set_test_option(forge_sort.TEST_FUSED, FUSED_MODE)
-    if first != FIRST_PASS[op]:
-        print(f"  first pass {first}, expected {FIRST_PASS[op]}", flush=True)
+        sorter.set_test_option(forge_sort.TEST_TOP16, TOP16_MODE)
+    expect = FIRST_PASS[op]
+    if top16 and dist == "same":
+        expect = forge_sort.FIRST_FUSED_OVERFLOW      # every digit constant: no pass after the fused one
+    if first != expect:
+        print(f"  first pass {first}, expected {expect}", flush=True)
         ok = False
     if dist == "same" and passes != 0:
         print(f"  equal keys ran {passes} passes", flush=True)
@@ -331,6 +352,7 @@ def main():
     if os.environ.get("EMU_TEST_UPSWEEP_PER_CU"):
         sorter.set_test_option(forge_sort.TEST_UPSWEEP_BLOCKS_PER_CU, int(os.environ["EMU_TEST_UPSWEEP_PER_CU"]))
     sorter.set_test_option(forge_sort.TEST_FUSED, FUSED_MODE)
+    sorter.set_test_option(forge_sort.TEST_TOP16, TOP16_MODE)
     print("tiles", sorter.tile_config(), flush=True)
     ok = True
     for spec in sys.argv[2:]:
