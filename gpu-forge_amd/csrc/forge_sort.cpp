@@ -88,6 +88,7 @@ struct fs_sorter {
     bool force_wide = false;             // 64-bit look-back entries for any n
     uint32_t fused_mode = 0;             // FS_TEST_FUSED: 0 by size, 1 never, 2 always
     uint32_t top16_mode = 0;             // FS_TEST_TOP16: 0 by size, 1 never, 2 always
+    uint32_t seg_bits = 0;               // FS_TEST_SEG_BITS: 0 by size, else the segment bits
     // the last sort's schedule (the sorter's, or the static scratch's) and
     // whether it began with the fused first pass
     uint32_t* last_plan = nullptr;
@@ -318,7 +319,14 @@ static bool top16_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
     if (op != FS_OP_SORT || (t != FS_KEY_U32 && t != FS_KEY_I32) || s->top16_mode == 1u || n < 2) return false;
     if (n > (1ull << 31) || s->fused_mode == 1u) return false;
     if (FS_FUSED_S1_KEYS(fused_sub_keys(n, s->tile[FS_VAR_K32])) >= (1ull << 32)) return false;
-    return s->top16_mode == 2u || n >= FS_TOP16_MIN_KEYS;
+    if (s->top16_mode == 2u) return true;
+    // By size: the 2^16 segments of a uniform input must fit a block with a
+    // margin of five standard deviations (local_keys - 5 sqrt(local_keys)
+    // keys each on average), so that hardly any takes the big-segment path.
+    uint64_t root = 0;
+    while ((root + 1) * (root + 1) <= s->local_keys) ++root;
+    const uint64_t mean_max = s->local_keys > 5 * root ? s->local_keys - 5 * root : 0;
+    return n >= FS_TOP16_MIN_KEYS && n <= (mean_max << 16);
 }
 
 // Bits that name a segment of the local sort: a uniform input's segment then
@@ -473,7 +481,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.s1_keys = fused ? (uint32_t)FS_FUSED_S1_KEYS(sub_keys) : 0u;
     a.sdigit = top16 ? 2u : 0u;
     a.segc = top16 ? sc.segc : 0u;
-    a.seg_bits = top16 ? seg_bits_for(n, s->local_keys) : 0u;
+    a.seg_bits = top16 ? (s->seg_bits ? s->seg_bits : seg_bits_for(n, s->local_keys)) : 0u;
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 #ifdef FS_FAULT_INJECTION
@@ -860,6 +868,11 @@ fs_status fs_sorter_set_test_option(fs_sorter* s, fs_test_option opt, uint64_t v
         case FS_TEST_TOP16:
             if (value > 2) return set_err(s, FS_ERR_INVALID_ARGUMENT, "top-16 mode %llu > 2", (unsigned long long)value);
             s->top16_mode = (uint32_t)value;
+            return FS_OK;
+        case FS_TEST_SEG_BITS:
+            if (value != 0 && (value < 8 || value > 16))
+                return set_err(s, FS_ERR_INVALID_ARGUMENT, "segment bits %llu outside 8..16", (unsigned long long)value);
+            s->seg_bits = (uint32_t)value;
             return FS_OK;
         case FS_TEST_UPSWEEP_BLOCKS_PER_CU:
             if (value > 64) return set_err(s, FS_ERR_INVALID_ARGUMENT, "upsweep blocks per CU %llu > 64",

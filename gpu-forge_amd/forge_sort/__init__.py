@@ -35,7 +35,8 @@ KEY_SIZE = {"u32": 4, "i32": 4, "f32": 4, "u64": 8, "i64": 8, "f64": 8}   # Sort
 OP_SORT, OP_ARGSORT, OP_PAIRS = 0, 1, 2
 NO_ALLOC_MAX_KEYS = 1 << 20          # FS_NO_ALLOC_MAX_KEYS
 # fs_test_option and the FS_FAULT_* codes (include/forge_sort.h, csrc/fs_params.h)
-TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT, TEST_FUSED, TEST_TOP16 = 0, 1, 2, 3, 4
+TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT, TEST_FUSED, TEST_TOP16, TEST_SEG_BITS = \
+    0, 1, 2, 3, 4, 5
 FUSED_BY_SIZE, FUSED_NEVER, FUSED_ALWAYS = 0, 1, 2       # TEST_FUSED values
 TOP16_BY_SIZE, TOP16_NEVER, TOP16_ALWAYS = 0, 1, 2       # TEST_TOP16 values
 FUSED_MIN_KEYS = 1 << 25                                 # FS_FUSED_MIN_KEYS
@@ -386,7 +387,7 @@ class GpuSorter:
 
     def set_test_option(self, option, value):
         """Testing hooks (TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU,
-        TEST_INJECT_FAULT, TEST_FUSED, TEST_TOP16): reach layouts the product uses only
+        TEST_INJECT_FAULT, TEST_FUSED, TEST_TOP16, TEST_SEG_BITS): reach layouts the product uses only
         at sizes too large for a test, choose the first pass, or inject a
         device-side fault (emulator builds)."""
         self._check(_load().fs_sorter_set_test_option(self._h, option, value))

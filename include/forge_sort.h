@@ -225,9 +225,11 @@ typedef enum fs_test_option {
     FS_TEST_FUSED = 3,                  /* keys-only sorts begin with the fused first pass:
                                            0 = from FS_FUSED_MIN_KEYS keys on (the default),
                                            1 = never, 2 = at every size */
-    FS_TEST_TOP16 = 4                   /* keys-only u32/i32 sorts take the top-16 path:
+    FS_TEST_TOP16 = 4,                  /* keys-only u32/i32 sorts take the top-16 path:
                                            0 = from FS_TOP16_MIN_KEYS keys on (the default),
                                            1 = never, 2 = at every size of at least 2 keys */
+    FS_TEST_SEG_BITS = 5                /* top-16 path: 0 = segment bits by size (the default),
+                                           8..16 = segments named by that many top bits */
 } fs_test_option;
 fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t value);
 
@@ -237,8 +239,9 @@ fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t v
  * (measured for u32 and u64 keys). */
 #define FS_FUSED_MIN_KEYS 33554432u
 
-/* Keys-only u32 and i32 sorts from this many keys on (up to 2^31) take the
- * top-16 path: the fused first pass on the second-highest byte, one stable
+/* Keys-only u32 and i32 sorts from this many keys on, up to 2^16 times the
+ * keys a local-sort block holds less five standard deviations (279,707,648
+ * keys with the gfx950 build's 4,608-key blocks), take the top-16 path: the fused first pass on the second-highest byte, one stable
  * pass on the highest byte, then a local sort of every segment of keys that
  * share their top bits, in LDS - three reads and writes of the keys instead of
  * four.  f32 keys keep the LSD passes (their exponent bytes make segments

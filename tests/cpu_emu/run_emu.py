@@ -278,6 +278,8 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
     sorter.set_test_option(forge_sort.TEST_FUSED,
                            forge_sort.FUSED_NEVER if op == "nofused" else forge_sort.FUSED_ALWAYS)
     sorter.set_test_option(forge_sort.TEST_TOP16, forge_sort.TOP16_ALWAYS if top16 else forge_sort.TOP16_NEVER)
+    # top16s<bits>: segments named by that many top bits
+    sorter.set_test_option(forge_sort.TEST_SEG_BITS, int(op[6:]) if op.startswith("top16s") else 0)
     try:
         ok = sorted_ok(sorter, kind, keys)
         first = sorter.first_pass()
@@ -285,7 +287,8 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
     finally:
         sorter.set_test_option(forge_sort.TEST_FUSED, FUSED_MODE)
         sorter.set_test_option(forge_sort.TEST_TOP16, TOP16_MODE)
-    expect = FIRST_PASS[op]
+        sorter.set_test_option(forge_sort.TEST_SEG_BITS, 0)
+    expect = FIRST_PASS["top16" if op.startswith("top16s") else op]
     if top16 and dist == "same":
         expect = forge_sort.FIRST_FUSED_OVERFLOW      # every digit constant: no pass after the fused one
     if first != expect:
@@ -299,7 +302,7 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
 
 
 def check(sorter, op, kind, n, dist, seed):
-    if op in FIRST_PASS:
+    if op in FIRST_PASS or op.startswith("top16s"):
         return check_first_pass(sorter, op, kind, n, dist, seed)
     if op == "noalloc":
         ok = check_no_alloc(sorter, kind, n, dist, seed)
