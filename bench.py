@@ -7,9 +7,11 @@ W + K copies of the same seeded input are prepared before timing, so the timed
 region holds exactly K back-to-back sorts and no copies (and no profiling
 events).  Per-launch kernel durations come from K more sorts of the same
 input, with HIP events that the library records around every launch on the
-stream the kernels run on (fs_set_profiling); the dominant kernel is the digit pass
-(fs_onesweep_k32), whose algorithmic traffic is one read and one write of
-every key per pass: 8 B/key (the 36 B/key whole-sort convention counts 4 such
+stream the kernels run on (fs_set_profiling).  A sort is a fixed sequence of
+launches; the roofline is reported for the launch position with the longest
+average duration (the dominant kernel): on the headline's top-16 path the
+local sort fs_local_k32, whose algorithmic traffic is one read and one write
+of every key, 8 B/key (the 36 B/key whole-sort convention counts 4 such
 passes plus one 4 B/key histogram read).
 
 The CPU baseline times the oracle (a scalar C restatement of the reference's
@@ -52,7 +54,9 @@ METRIC = "Mkeys/s (u32 256M, 1 MI355X) and % of HBM-bandwidth roofline vs host C
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 PASS_BYTES_PER_KEY = 8         # one read + one write of a u32 key per digit pass
 SORT_BYTES_PER_KEY = 36        # k + k*2*k for k = 4 (histogram read + 4 passes)
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fs_onesweep_k32_u32_256M_traffic.json")
+# measured HBM bytes per launch of the headline's dominant kernel (rocprofv3
+# FETCH_SIZE / WRITE_SIZE, scaled by a copy kernel's readings)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "{kernel}_u32_256M_traffic.json")
 
 
 # name -> (op, key type, n, data description, BASELINE.json config)
@@ -204,12 +208,30 @@ def _cpu_model():
             f"model {info.get('model', '?')}, stepping {info.get('stepping', '?')})")
 
 
-def load_traffic():
+def load_traffic(kernel):
     try:
-        with open(TRAFFIC_FILE) as f:
-            return json.load(f)
+        with open(TRAFFIC_FILE.format(kernel=kernel)) as f:
+            t = json.load(f)
     except (OSError, ValueError):
         return None
+    return t if t.get("kernel", kernel) == kernel else None
+
+
+def launch_bytes(name, ksize, vbytes, n):
+    """Algorithmic bytes of one launch that does its work: a histogram read
+    reads every key; the fused first pass, a digit pass and the local sort
+    read and write every key (and value)."""
+    if name.startswith("fs_upsweep"):
+        return ksize * n
+    if name.startswith(("fs_first", "fs_local")):
+        return 2 * ksize * n
+    if name.startswith("fs_onesweep"):
+        return 2 * (ksize + vbytes) * n
+    return 0
+
+
+FIRST_KINDS = ["histogram read", "fused first pass", "fused first pass, region overflow",
+               "top-16 path", "top-16 path, region overflow (re-scatter)"]
 
 
 def main():
@@ -278,7 +300,6 @@ def main():
     sorter.synchronize()
     sorter.device_synchronize()
     t1 = time.perf_counter()
-    _, digit_mask = sorter.last_pass_info()      # digits whose pass ran (same input every step)
     first_kind = sorter.first_pass()             # how each sort began (same input every step)
     log(f"bench: timed {K} sorts in {t1 - t0:.4f} s")
     # the last timed output (sorted, same multiset, stable for argsort and
@@ -320,46 +341,42 @@ def main():
     ms_per_step = (t1 - t0) * 1e3 / K
     value = n / (ms_per_step / 1e3) / 1e6
 
-    # Digit-pass kernel and algorithmic bytes (one read + one write of every
-    # key and value per pass; whole sort B(k,v) = k + 2k(k+v) per key).
+    # Launch sequence of one sort (the same for every sort of this input) and
+    # the algorithmic bytes per key of the whole sort, B(k,v) = k + 2k(k+v).
     vbytes = 4 if op != OP_SORT else 0
-    pass_kernel = "fs_onesweep_" + ("k64" if ksize == 8 else "k32") + ("_v" if vbytes else "")
-    pass_bytes = 2 * (ksize + vbytes)
     sort_bytes = ksize + 2 * ksize * (ksize + vbytes)
+    L = len(prof) // K
+    seq = [{"kernel": prof[j][0], "avg_ms": round(float(np.mean([prof[s * L + j][1] for s in range(K)])), 4)}
+           for j in range(L)]
     by_kernel = {}
     for name, ms in prof:
         by_kernel.setdefault(name, []).append(ms)
-    # every sort launches one digit pass per digit position, in digit order; a
-    # constant digit's launch exits at once and is not averaged.  Keys-only
-    # sorts launch digit 0 on the any-order kernel (or sort it in the fused
-    # first pass), so the stable kernel runs digits 1.. there.
-    digits = ksize                                 # 8-bit digits: one per key byte
-    pass_digits = list(range(1 if op == OP_SORT else 0, digits))
-    passes = by_kernel.get(pass_kernel, [])
-    active = [ms for i, ms in enumerate(passes) if digit_mask >> pass_digits[i % len(pass_digits)] & 1]
-    pass_ms = float(np.mean(active)) if active else float("nan")
-    achieved = pass_bytes * n / (pass_ms / 1e3) / 1e9
+    kernels = {k: {"avg_ms": round(float(np.mean(v)), 4), "launches": len(v)}
+               for k, v in sorted(by_kernel.items())}
     kernel_sum_ms = sum(ms for _, ms in prof) / K
-    traffic = load_traffic() if headline else None
+    # the dominant kernel: the launch position with the longest average
+    dom = max(range(L), key=lambda j: seq[j]["avg_ms"])
+    dom_kernel, dom_ms = seq[dom]["kernel"], seq[dom]["avg_ms"]
+    dom_bytes = launch_bytes(dom_kernel, ksize, vbytes, n)
+    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+    traffic = load_traffic(dom_kernel) if headline else None
     roofline = {
-        "bound": "hbm", "kernel": pass_kernel,
+        "bound": "hbm", "kernel": dom_kernel,
         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic.get("bytes_per_launch") if traffic else None,
-        "bytes_per_launch_algorithmic": pass_bytes * n,
-        "avg_launch_ms": round(pass_ms, 4), "launches": len(active),
+        "bytes_per_launch_algorithmic": dom_bytes,
+        "avg_launch_ms": dom_ms, "launch_position": dom,
     }
-    kernels = {k: {"avg_ms": round(float(np.mean(v)), 4), "launches": len(v)}
-               for k, v in sorted(by_kernel.items())}
-    # the first kernel of each sort: the fused first pass (one read and one
-    # write of every key, the other digits counted on the way) or the histogram
-    # read (one read of every key)
-    first_kernel = ("fs_first_" if first_kind else "fs_upsweep_") + ("k64" if ksize == 8 else "k32")
-    first_ms = float(np.mean(by_kernel[first_kernel])) if by_kernel.get(first_kernel) else float("nan")
-    first_bytes = (2 if first_kind else 1) * ksize * n
-    first_pass = {"kind": ["histogram read", "fused first pass", "fused first pass, region overflow"][first_kind],
-                  "kernel": first_kernel, "avg_ms": round(first_ms, 4), "bytes_algorithmic": first_bytes,
-                  "achieved_GBps": round(first_bytes / (first_ms / 1e3) / 1e9, 1)}
+    for j, e in enumerate(seq):
+        b = launch_bytes(e["kernel"], ksize, vbytes, n)
+        # (a launch far shorter than its bytes allow had nothing to do: a
+        # constant digit's, or the re-scatter launch without an overflow)
+        if b and e["avg_ms"] > 0 and b / (e["avg_ms"] / 1e3) / 1e9 <= HBM_PEAK_GBS:
+            e["achieved_GBps"] = round(b / (e["avg_ms"] / 1e3) / 1e9, 1)
+    first_pass = {"kind": FIRST_KINDS[first_kind] if first_kind < len(FIRST_KINDS) else str(first_kind),
+                  "kernel": seq[0]["kernel"] if seq[0]["kernel"].startswith(("fs_first", "fs_upsweep"))
+                  else seq[1]["kernel"]}
     sort_frac = sort_bytes * n / (ms_per_step / 1e3) / (HBM_PEAK_GBS * 1e9)
 
     # The slice API (sort_u32 on a host array: copy in, sort, copy out), reported
@@ -410,6 +427,7 @@ def main():
         "oracle_match": cpu["oracle_match"] if cpu else None,
         "exact_match": cpu["oracle_match"] if cpu else exact,
         "first_pass": first_pass,
+        "launch_sequence": seq,
         "kernels": kernels, "kernel_ms_per_step": round(kernel_sum_ms, 4),
         "slice_api": slice_api,
         "cpu_baseline": cpu,

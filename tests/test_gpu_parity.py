@@ -137,6 +137,15 @@ def make_keys(kind, n, dist, seed, tile=None):
         b = g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False)
         in0 = (np.arange(n) // tile // 8) % 8 == 0
         b[in0] = (b[in0] & ~BITS[kind](0xFF)) | BITS[kind](3)
+    elif dist == "grp2":        # byte 2 is 3 in the tiles of region group 0 (the top-16 path's fused pass)
+        b = g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False)
+        in0 = (np.arange(n) // tile // 8) % 8 == 0
+        b[in0] = (b[in0] & ~BITS[kind](0xFF0000)) | BITS[kind](0x30000)
+    elif dist == "top8":        # the top byte only two values: segments far larger than a block holds
+        b = g.integers(0, 1 << 24, size=n, dtype=BITS[kind])
+        b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](24)
+    elif dist == "zipf":        # Zipf(1.1) ranks below 2^20: a few huge segments, many tiny ones
+        b = np.minimum(g.zipf(1.1, size=n) - 1, (1 << 20) - 1).astype(BITS[kind])
     else:
         raise ValueError(dist)
     keys = b.view(NP[kind])
@@ -342,12 +351,99 @@ def test_fused_first_pass(sorter, kind, n, dist, expect):
         sorter.set_test_option(TEST_FUSED, FUSED_BY_SIZE)
 
 
-@pytest.mark.parametrize("n,expect", [(1 << 25, 1), ((1 << 25) - 1, 0), (1 << 20, 0)])
-def test_fused_first_pass_by_size(sorter, n, expect):
-    """By default the fused first pass starts at FS_FUSED_MIN_KEYS keys."""
-    keys = datagen.uniform_u32(n, seed=950)
-    check_buffer(sorter, "u32", keys)
+@pytest.mark.parametrize("kind,n,expect", [("u32", 1 << 25, 3), ("f32", 1 << 25, 1), ("u32", (1 << 25) - 1, 0),
+                                            ("u32", 1 << 20, 0)])
+def test_fused_first_pass_by_size(sorter, kind, n, expect):
+    """By default the fused first pass starts at FS_FUSED_MIN_KEYS keys,
+    where u32/i32 keys take the top-16 path (FS_TOP16_MIN_KEYS)."""
+    keys = make_keys(kind, n, "uniform", seed=950)
+    check_buffer(sorter, kind, keys)
     assert sorter.first_pass() == expect
+
+
+# ---- the top-16 path of keys-only u32/i32 sorts -------------------------------------
+
+TOP16_CASES = [
+    # trivial, ragged and mid sizes (segments of the top 8 bits up to 16)
+    (2, "uniform", 3), (100, "uniform", 3), (4097, "uniform", 3), (1_000_003, "uniform", 3),
+    (16_777_216, "uniform", 3),
+    # sorted input: each digit-2 value comes in one short run per digit-3
+    # value, so the region groups' shares of it vary and a region may
+    # overflow (3 or 4)
+    (5_000_000, "sorted", (3, 4)), (3_000_001, "reverse", (3, 4)),
+    # constant digits: only the lowest varies, only the low 12 bits vary, a
+    # few values; skewed segments (Zipf ranks, two top-byte values) larger
+    # than a block holds, sorted a digit at a time by their block
+    (300_007, "byte0", 3), (2_000_000, "lowbits", 3), (1_000_000, "few", 3), (2_000_003, "zipf", 3),
+    (3_000_000, "top8", 3),
+    # a region of the fused pass overflows (byte 2 crowded into region
+    # group 0): its second launch re-scatters into exact regions
+    (2_000_000, "grp2", 4), (17_000_000, "grp2", 4),
+    # every digit constant: no pass after the fused one
+    (100_003, "same", 2),
+]
+
+
+@pytest.mark.parametrize("kind", ["u32", "i32"])
+@pytest.mark.parametrize("n,dist,expect", TOP16_CASES)
+def test_top16_path(sorter, kind, n, dist, expect):
+    """Keys-only u32/i32 sorts on the top-16 path (fused pass on digit 2,
+    stable pass on digit 3 counting the segments, local sort of each
+    segment), forced at every size: exact against the oracle through the
+    slice and buffer APIs, and beginning the way the case names."""
+    from forge_sort import TEST_TOP16, TOP16_ALWAYS, TOP16_BY_SIZE
+    keys = make_keys(kind, n, dist, seed=960 + n % 89, tile=sorter.tile_config()["k32"])
+    sorter.set_test_option(TEST_TOP16, TOP16_ALWAYS)
+    try:
+        expect = expect if isinstance(expect, tuple) else (expect,)
+        check_sort(sorter, kind, keys)
+        assert sorter.first_pass() in expect
+        check_buffer(sorter, kind, keys)
+        assert sorter.first_pass() in expect
+    finally:
+        sorter.set_test_option(TEST_TOP16, TOP16_BY_SIZE)
+
+
+@pytest.mark.parametrize("bits", [8, 11, 12, 13, 14, 15, 16])
+@pytest.mark.parametrize("dist", ["uniform", "few"])
+def test_top16_segment_bits(sorter, bits, dist):
+    """Every local-sort plan (the segment bits set how many low bits each
+    block sorts: 16 bits as 10 + 6, 17-19 as the rest + 8, more as the rest
+    + 8 + 8), and segments that are empty, tiny or larger than a block."""
+    from forge_sort import TEST_SEG_BITS, TEST_TOP16, TOP16_ALWAYS, TOP16_BY_SIZE
+    keys = make_keys("u32", 3_000_017, dist, seed=970 + bits)
+    sorter.set_test_option(TEST_TOP16, TOP16_ALWAYS)
+    sorter.set_test_option(TEST_SEG_BITS, bits)
+    try:
+        check_buffer(sorter, "u32", keys)
+        assert sorter.first_pass() == 3
+    finally:
+        sorter.set_test_option(TEST_SEG_BITS, 0)
+        sorter.set_test_option(TEST_TOP16, TOP16_BY_SIZE)
+
+
+def test_top16_size_limit(sorter):
+    """The largest input the top-16 path takes by size (its segments of a
+    uniform input within a block's keys, with a five-sigma margin) and one
+    key more (the fused LSD passes): ascending, same multiset."""
+    import math
+    local = 256 * 18                                   # keys of a local-sort block (gfx950 build)
+    limit = (local - 5 * math.isqrt(local)) << 16
+    for n, expect in ((limit, 3), (limit + 1, 1)):
+        keys = datagen.uniform_u32(n, seed=980)
+        k64 = keys.astype(np.uint64)
+        s_sum, s_xor = int(k64.sum()), int(np.bitwise_xor.reduce(keys))
+        del k64
+        buf = sorter.alloc_sort_buffer("u32", n)
+        buf.copy_from_slice(keys)
+        del keys
+        sorter.sort_buffer(buf)
+        assert sorter.first_pass() == expect
+        out = buf.as_slice()
+        buf.free()
+        assert bool(np.all(out[1:] >= out[:-1])), "not ascending"
+        assert (int(out.astype(np.uint64).sum()), int(np.bitwise_xor.reduce(out))) == (s_sum, s_xor)
+        del out
 
 
 def test_fused_first_pass_2_31_keys(sorter):
