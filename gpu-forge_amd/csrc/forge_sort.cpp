@@ -87,7 +87,7 @@ struct fs_sorter {
     // Test options (fs_sorter_set_test_option); defaults give the product layout.
     bool force_wide = false;             // 64-bit look-back entries for any n
     uint32_t fused_mode = 0;             // FS_TEST_FUSED: 0 by size, 1 never, 2 always
-    uint32_t top16_mode = 0;             // FS_TEST_TOP16: 0 by size, 1 never, 2 always
+    uint32_t top16_mode = 0;             // FS_TEST_TOP16: 0 by size, 1 never, 2 always (even skewed), 3 sampled
     uint32_t seg_bits = 0;               // FS_TEST_SEG_BITS: 0 by size, else the segment bits
     // the last sort's schedule (the sorter's, or the static scratch's) and
     // whether it began with the fused first pass
@@ -319,7 +319,7 @@ static bool top16_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
     if (op != FS_OP_SORT || (t != FS_KEY_U32 && t != FS_KEY_I32) || s->top16_mode == 1u || n < 2) return false;
     if (n > (1ull << 31) || s->fused_mode == 1u) return false;
     if (FS_FUSED_S1_KEYS(fused_sub_keys(n, s->tile[FS_VAR_K32])) >= (1ull << 32)) return false;
-    if (s->top16_mode == 2u) return true;
+    if (s->top16_mode >= 2u) return true;
     // By size: the 2^16 segments of a uniform input must fit a block with a
     // margin of five standard deviations (local_keys - 5 sqrt(local_keys)
     // keys each on average), so that hardly any takes the big-segment path.
@@ -479,9 +479,11 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.fused = fused ? 1u : 0u;
     a.sub_keys = fused ? (uint32_t)sub_keys : 0u;
     a.s1_keys = fused ? (uint32_t)FS_FUSED_S1_KEYS(sub_keys) : 0u;
-    a.sdigit = top16 ? 2u : 0u;
     a.segc = top16 ? sc.segc : 0u;
     a.seg_bits = top16 ? (s->seg_bits ? s->seg_bits : seg_bits_for(n, s->local_keys)) : 0u;
+    // a segment the region sample estimates above 16 blocks' keys sends the
+    // sort to the LSD passes (unless a test forces the top-16 path)
+    a.seg_limit = s->top16_mode == 2u ? 0xFFFFFFFFu : 16u * s->local_keys;
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 #ifdef FS_FAULT_INJECTION
@@ -491,11 +493,14 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
 #endif
 
     void* args1[] = {&a};
-    if (top16) {
-        // region sample (digit 2) -> fused pass (digit 2) -> its re-scatter
-        // launch (works only after an overflow) -> the stable pass on digit 3
-        // (launch slot 0) -> the local sort, one block per segment
-        if ((r = launch(s, K_SAMPLE32, 1, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK) return r;
+    if (fused) {
+        // region sample (it picks the scatter digit: 2 on the top-16 path
+        // unless the sample shows oversized segments, else 0) -> fused pass ->
+        // its re-scatter launch (works only after an overflow) -> the digit
+        // passes in launch slots 0 .. digits-2 -> (top-16 launch sequence) the
+        // local sort, one block per segment
+        if ((r = launch(s, key64(t) ? K_SAMPLE64 : K_SAMPLE32, 1, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK)
+            return r;
         unsigned grid = num_tiles;
 #ifdef FS_FAULT_INJECTION
         if (s->fault == FS_FAULT_EXTRA_BLOCK) grid += 1u;
@@ -503,31 +508,25 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         for (uint32_t l = 0; l < 2; ++l) {
             uint32_t which = l;
             void* argsf[] = {&a, &which};
-            if ((r = launch(s, K_FIRST32, l ? num_tiles : grid, s->block[var], argsf, st, no_alloc)) != FS_OK) return r;
+            if ((r = launch(s, key64(t) ? K_FIRST64 : K_FIRST32, l ? num_tiles : grid, s->block[var], argsf, st,
+                            no_alloc)) != FS_OK)
+                return r;
         }
-        uint32_t slot = 0;
-        void* args2[] = {&a, &slot};
-        if ((r = launch(s, K_OS32, num_tiles, s->block[var], args2, st, no_alloc)) != FS_OK) return r;
-        if ((r = launch(s, K_LOCAL32, 1u << a.seg_bits, s->local_block, args1, st, no_alloc)) != FS_OK) return r;
+        for (uint32_t sl = 0; sl + 1 < a.digits; ++sl) {
+            uint32_t slot = sl;
+            void* args2[] = {&a, &slot};
+            if ((r = launch(s, K_OS32 + var, num_tiles, s->block[var], args2, st, no_alloc)) != FS_OK) return r;
+        }
+        if (top16 && (r = launch(s, K_LOCAL32, 1u << a.seg_bits, s->local_block, args1, st, no_alloc)) != FS_OK)
+            return r;
         s->last_stream = st;
         s->pending = true;
         s->last_plan = (uint32_t*)(uintptr_t)sc.plan;
         s->last_fused = true;
-        s->last_top16 = true;
+        s->last_top16 = top16;
         return FS_OK;
     }
-    if (fused) {
-        if ((r = launch(s, key64(t) ? K_SAMPLE64 : K_SAMPLE32, 1, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK)
-            return r;
-        unsigned grid = num_tiles;
-#ifdef FS_FAULT_INJECTION
-        if (s->fault == FS_FAULT_EXTRA_BLOCK) grid += 1u;
-#endif
-        uint32_t first_launch = 0;
-        void* argsf[] = {&a, &first_launch};
-        if ((r = launch(s, key64(t) ? K_FIRST64 : K_FIRST32, grid, s->block[var], argsf, st, no_alloc)) != FS_OK)
-            return r;
-    } else {
+    {
         const unsigned up_grid = (unsigned)up_blocks;
         if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK) return r;
     }
@@ -540,14 +539,14 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         const int k = (d == 0 && op == FS_OP_SORT) ? (key64(t) ? K_ANY64 : K_ANY32) : os;
         unsigned grid = num_tiles;
 #ifdef FS_FAULT_INJECTION
-        if (s->fault == FS_FAULT_EXTRA_BLOCK && d == 0 && !fused) grid += 1u;
+        if (s->fault == FS_FAULT_EXTRA_BLOCK && d == 0) grid += 1u;
 #endif
         if ((r = launch(s, k, grid, s->block[var], args2, st, no_alloc)) != FS_OK) return r;
     }
     s->last_stream = st;
     s->pending = true;
     s->last_plan = (uint32_t*)(uintptr_t)sc.plan;
-    s->last_fused = fused;
+    s->last_fused = false;
     s->last_top16 = false;
     return FS_OK;
 }
@@ -866,7 +865,7 @@ fs_status fs_sorter_set_test_option(fs_sorter* s, fs_test_option opt, uint64_t v
             s->fused_mode = (uint32_t)value;
             return FS_OK;
         case FS_TEST_TOP16:
-            if (value > 2) return set_err(s, FS_ERR_INVALID_ARGUMENT, "top-16 mode %llu > 2", (unsigned long long)value);
+            if (value > 3) return set_err(s, FS_ERR_INVALID_ARGUMENT, "top-16 mode %llu > 3", (unsigned long long)value);
             s->top16_mode = (uint32_t)value;
             return FS_OK;
         case FS_TEST_SEG_BITS:
@@ -1038,7 +1037,7 @@ fs_status fs_sorter_first_pass(fs_sorter* s, uint32_t* kind) {
     if (s->last_top16 && (mask & FS_MASK_TOP16))
         *kind = w[FS_PLAN_RESCATTER] ? 4u : 3u;
     else
-        *kind = !s->last_fused ? 0u : (mask & FS_MASK_FUSED) ? 1u : 2u;
+        *kind = !s->last_fused ? 0u : ((mask & FS_MASK_FUSED) && !w[FS_PLAN_RESCATTER]) ? 1u : 2u;
     return FS_OK;
 }
 

@@ -183,8 +183,9 @@
 // Region table words (bases, total, caps), and the sample: FS_SAMPLE_CHUNKS
 // runs of FS_SAMPLE_CHUNK consecutive keys spread evenly over the input (all
 // keys when there are fewer).
-#define FS_RTABLE_WORDS (FS_REGIONS + 1 + FS_RADIX)
+#define FS_RTABLE_WORDS (FS_REGIONS + 2 + FS_RADIX)
 #define FS_RTABLE_CAPS (FS_REGIONS + 1)
+#define FS_RTABLE_SDIGIT (FS_REGIONS + 1 + FS_RADIX)   // the digit the fused pass scatters by
 #define FS_SAMPLE_CHUNKS 256
 #define FS_SAMPLE_CHUNK 128
 // S1 keys the fused pass's regions may take for region groups of at most
@@ -244,16 +245,23 @@
 #define FS_PLAN_WORDS (FS_PLAN_NPASSES + 8)
 
 // Top-16 path of keys-only 32-bit sorts (from FS_TOP16_MIN_KEYS keys): the
-// fused first pass scatters by digit 2 (FsArgs.sdigit) into its regions, a
+// fused first pass scatters by digit 2 (the region sample's choice,
+// FS_RTABLE_SDIGIT) into its regions, a
 // stable pass on digit 3 reads the regions in digit-2 order - so its output is
 // ordered by the top 16 bits - and counts the keys of every top-16-bit value
 // (FS_SEGS counters), and the local sort (fs_local_*) sorts each segment of
 // keys sharing their top seg_bits bits, in LDS, by the bits below: one block
 // per segment, one read and one write of every key.  A segment larger than a
 // block holds is sorted by that block through scratch, a digit at a time.
-// seg_bits is chosen on the host so that a segment holds about
-// 2^FS_LOCAL_LOG2 keys of a uniform input.
+// seg_bits is chosen on the host so that a segment of a uniform input fits
+// a block.  The region sample estimates the segments from its keys (their
+// top seg_bits bits): one estimated above FsArgs.seg_limit keys (skewed or
+// constant top bytes) makes it choose digit 0 instead, and the same launches
+// run the LSD passes (the stable passes on digits 1-3 in the digit-pass
+// launches, the local sort's launch idle).
 #define FS_SEGS 65536u
+// a segment estimate counts only from this many sampled keys on
+#define FS_SEG_MIN_SAMPLES 8u
 #ifndef FS_L32_BLOCK
 #define FS_L32_BLOCK 256
 #endif
@@ -340,9 +348,11 @@ typedef struct FsArgs {
     uint32_t sub_keys;          // keys of the fullest region group (fused path), else 0
     uint32_t fused;             // 1: the sort starts with the fused first pass (keys-only)
     uint32_t s1_keys;           // keys S1 holds (fused path: the regions' budget), else 0
-    uint32_t sdigit;            // digit the fused pass scatters by (0; 2 on the top-16 path)
+    uint32_t seg_limit;         // top-16 path: the region sample takes the LSD passes instead when it
+                                // estimates a segment of more keys than this (0xFFFFFFFF: never)
     uint64_t segc;              // u32[FS_SEGS] keys per top-16-bit value (top-16 path; zero before its digit-3 pass)
-    uint32_t seg_bits;          // top-16 path: bits that name a segment of the local sort (8..16), else 0
+    uint32_t seg_bits;          // top-16 launch sequence: bits that name a segment of the local sort
+                                // (8..16), else 0
     uint32_t reserved0;
 } FsArgs;
 

@@ -38,7 +38,7 @@ NO_ALLOC_MAX_KEYS = 1 << 20          # FS_NO_ALLOC_MAX_KEYS
 TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT, TEST_FUSED, TEST_TOP16, TEST_SEG_BITS = \
     0, 1, 2, 3, 4, 5
 FUSED_BY_SIZE, FUSED_NEVER, FUSED_ALWAYS = 0, 1, 2       # TEST_FUSED values
-TOP16_BY_SIZE, TOP16_NEVER, TOP16_ALWAYS = 0, 1, 2       # TEST_TOP16 values
+TOP16_BY_SIZE, TOP16_NEVER, TOP16_ALWAYS, TOP16_SAMPLED = 0, 1, 2, 3   # TEST_TOP16 values
 FUSED_MIN_KEYS = 1 << 25                                 # FS_FUSED_MIN_KEYS
 TOP16_MIN_KEYS = 1 << 25                                 # FS_TOP16_MIN_KEYS
 # fs_sorter_first_pass: how the last sort began
@@ -394,8 +394,9 @@ class GpuSorter:
 
     def first_pass(self):
         """How the last sort began: FIRST_HISTOGRAM, FIRST_FUSED (the fused
-        first pass, regions used), FIRST_FUSED_OVERFLOW (a region overflowed;
-        stable passes over the caller's keys followed), FIRST_TOP16 (the top-16
+        first pass, regions used), FIRST_FUSED_OVERFLOW (a region overflowed
+        and the keys were re-scattered into exact regions, or every digit is
+        constant), FIRST_TOP16 (the top-16
         path) or FIRST_TOP16_RESCATTER (the top-16 path after a region
         overflowed, its keys re-scattered into exact regions)."""
         k = ctypes.c_uint32()

@@ -6,6 +6,7 @@
 Both land in-tree so that they travel with the repository snapshot.
 """
 import os
+import re
 import subprocess
 import sys
 
@@ -30,11 +31,33 @@ def _run(cmd):
     subprocess.run(cmd, check=True)
 
 
+def _check_no_spills(report):
+    """Every kernel must keep its registers: a build in which the fused pass
+    spilled to scratch gave wrong results on the GPU (the same source ran
+    exact in the CPU emulator), so a spill fails the build."""
+    name, bad = None, []
+    for line in report.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            bad.append(f"{name} ({m.group(1)} bytes/lane)")
+    if bad:
+        raise RuntimeError("kernels spill registers to scratch: " + ", ".join(bad))
+
+
 def build(verbose=True):
     os.makedirs(LIBDIR, exist_ok=True)
     tmp = HSACO + ".tmp"
-    _run([os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS,
-          "-I", CSRC, "-o", tmp, os.path.join(CSRC, "radix_kernels.hip")])
+    cmd = [os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, "-Rpass-analysis=kernel-resource-usage",
+           "-I", CSRC, "-o", tmp, os.path.join(CSRC, "radix_kernels.hip")]
+    print("+", " ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stderr)
+        raise subprocess.CalledProcessError(r.returncode, cmd)
+    _check_no_spills(r.stderr)
     os.replace(tmp, HSACO)
     tmp = SO + ".tmp"
     _run(["g++", "-O2", "-g", "-std=c++17", "-shared", "-fPIC", "-Wall",

@@ -225,9 +225,12 @@ typedef enum fs_test_option {
     FS_TEST_FUSED = 3,                  /* keys-only sorts begin with the fused first pass:
                                            0 = from FS_FUSED_MIN_KEYS keys on (the default),
                                            1 = never, 2 = at every size */
-    FS_TEST_TOP16 = 4,                  /* keys-only u32/i32 sorts take the top-16 path:
+    FS_TEST_TOP16 = 4,                  /* keys-only u32/i32 sorts take the top-16 launch sequence:
                                            0 = from FS_TOP16_MIN_KEYS keys on (the default),
-                                           1 = never, 2 = at every size of at least 2 keys */
+                                           1 = never, 2 = at every size of at least 2 keys and
+                                           on the top-16 path even where its region sample
+                                           estimates oversized segments, 3 = at every size,
+                                           the sample choosing as by default */
     FS_TEST_SEG_BITS = 5                /* top-16 path: 0 = segment bits by size (the default),
                                            8..16 = segments named by that many top bits */
 } fs_test_option;
@@ -245,14 +248,18 @@ fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t v
  * pass on the highest byte, then a local sort of every segment of keys that
  * share their top bits, in LDS - three reads and writes of the keys instead of
  * four.  f32 keys keep the LSD passes (their exponent bytes make segments
- * too large for one block). */
+ * too large for one block), and so does an input whose region sample shows a
+ * segment of more than 16 blocks' keys (constant or skewed top bytes): the
+ * same launches then run the fused pass on the lowest byte and the stable
+ * passes on the others. */
 #define FS_TOP16_MIN_KEYS 33554432u
 
 /* How the last completed sort began: 0 = the histogram read (argsort, pairs,
  * and keys-only sorts outside the fused range), 1 = the fused first pass of a
  * keys-only sort, its regions read by the next pass,
- * 2 = the fused first pass, then stable passes over the caller's keys (a
- * region overflowed on a skewed lowest byte, or every digit is constant),
+ * 2 = the fused first pass after a region overflowed (the keys re-scattered
+ * into exact regions by its second launch), or every digit constant (no
+ * pass after it),
  * 3 = the top-16 path (fused pass on the second-highest byte, its regions
  * read by the pass on the highest byte, then the local sort),
  * 4 = the top-16 path after a region of its fused pass overflowed (the keys

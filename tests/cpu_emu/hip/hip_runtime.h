@@ -147,6 +147,12 @@ inline unsigned long long atomicAdd(unsigned long long* p, unsigned long long v)
     return __atomic_fetch_add(p, v, __ATOMIC_ACQ_REL);
 }
 inline uint32_t atomicOr(uint32_t* p, uint32_t v) { return __atomic_fetch_or(p, v, __ATOMIC_ACQ_REL); }
+inline uint32_t atomicMax(uint32_t* p, uint32_t v) {
+    uint32_t old = __atomic_load_n(p, __ATOMIC_ACQUIRE);
+    while (old < v && !__atomic_compare_exchange_n(p, &old, v, false, __ATOMIC_ACQ_REL, __ATOMIC_ACQUIRE)) {
+    }
+    return old;
+}
 inline unsigned long long atomicOr(unsigned long long* p, unsigned long long v) {
     return __atomic_fetch_or(p, v, __ATOMIC_ACQ_REL);
 }

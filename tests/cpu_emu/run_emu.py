@@ -74,6 +74,13 @@ def keys_for(kind, n, dist, seed, tile=None):
         # than a block holds
         b = g.integers(0, 1 << 24, size=n, dtype=BITS[kind])
         b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](24)
+    elif dist == "top8grp0":
+        # two top-byte values (the top-16 sequence's sample takes the LSD
+        # passes) and byte 0 crowded into region group 0 (its region overflows)
+        b = g.integers(0, 1 << 24, size=n, dtype=BITS[kind])
+        b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](24)
+        in0 = (np.arange(n) // tile // 8) % 8 == 0
+        b[in0] = (b[in0] & ~BITS[kind](0xFF)) | BITS[kind](3)
     elif dist == "zipf":
         # a dominant bin: Zipf(1.1) ranks below 2^20 (most keys small, digit 1
         # and 2 mostly zero), as in the pairs benchmark config
@@ -266,7 +273,10 @@ FUSED_MODE = int(os.environ.get("EMU_TEST_FUSED", "0"))
 TOP16_MODE = int(os.environ.get("EMU_TEST_TOP16", "0"))
 FIRST_PASS = {"fused": forge_sort.FIRST_FUSED, "fusedover": forge_sort.FIRST_FUSED_OVERFLOW,
               "nofused": forge_sort.FIRST_HISTOGRAM, "top16": forge_sort.FIRST_TOP16,
-              "top16over": forge_sort.FIRST_TOP16_RESCATTER}
+              "top16over": forge_sort.FIRST_TOP16_RESCATTER,
+              # the top-16 launch sequence, its sample choosing the LSD passes
+              "top16auto_lsd": forge_sort.FIRST_FUSED, "top16auto_lsdover": forge_sort.FIRST_FUSED_OVERFLOW,
+              "top16auto": forge_sort.FIRST_TOP16}
 
 
 def check_first_pass(sorter, op, kind, n, dist, seed):
@@ -277,7 +287,8 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
     top16 = op.startswith("top16")
     sorter.set_test_option(forge_sort.TEST_FUSED,
                            forge_sort.FUSED_NEVER if op == "nofused" else forge_sort.FUSED_ALWAYS)
-    sorter.set_test_option(forge_sort.TEST_TOP16, forge_sort.TOP16_ALWAYS if top16 else forge_sort.TOP16_NEVER)
+    sorter.set_test_option(forge_sort.TEST_TOP16, forge_sort.TOP16_SAMPLED if op.startswith("top16auto")
+                           else forge_sort.TOP16_ALWAYS if top16 else forge_sort.TOP16_NEVER)
     # top16s<bits>: segments named by that many top bits
     sorter.set_test_option(forge_sort.TEST_SEG_BITS, int(op[6:]) if op.startswith("top16s") else 0)
     try:
@@ -289,12 +300,12 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
         sorter.set_test_option(forge_sort.TEST_TOP16, TOP16_MODE)
         sorter.set_test_option(forge_sort.TEST_SEG_BITS, 0)
     expect = FIRST_PASS["top16" if op.startswith("top16s") else op]
-    if top16 and dist == "same":
-        expect = forge_sort.FIRST_FUSED_OVERFLOW      # every digit constant: no pass after the fused one
+    if top16 and dist == "same" and not op.startswith("top16auto"):
+        expect = forge_sort.FIRST_TOP16               # forced onto the top-16 path: one segment of every key
     if first != expect:
         print(f"  first pass {first}, expected {expect}", flush=True)
         ok = False
-    if dist == "same" and passes != 0:
+    if dist == "same" and passes != 0 and expect != forge_sort.FIRST_TOP16:
         print(f"  equal keys ran {passes} passes", flush=True)
         ok = False
     print(f"{'PASS' if ok else 'FAIL'} {op} {kind} n={n} {dist} passes={passes} mask={mask:#x}", flush=True)

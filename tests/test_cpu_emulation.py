@@ -221,3 +221,35 @@ def test_emulated_sanitizers(emulator):
                       "fused:u32:5000:byte0:42"],
               timeout=600, env={"LD_PRELOAD": libasan, "EMU_NO_SEGV_HANDLER": "1", "EMU_CUS": "4", "EMU_TEST_FUSED": "2",
                                 "ASAN_OPTIONS": "detect_leaks=0:detect_stack_use_after_return=0"})
+
+
+TOP16_SMALL = [
+    # the top-16 launch sequence forced at every size (tiny local-sort blocks
+    # of 512 keys in the small build): every plan of the local sort through
+    # the segment bits, ragged and tiny inputs, constant digits, segments
+    # larger than a block (big-segment path), an overflowing region of the
+    # fused pass on digit 2 (re-scattered by its second launch)
+    "top16:u32:5000:uniform:1", "top16:i32:20000:uniform:2", "top16:u32:2:uniform:3", "top16:u32:100:uniform:4",
+    "top16:u32:1025:uniform:5", "top16:u32:3000:low12:6", "top16:u32:9000:zipf:7", "top16:u32:20000:top8:8",
+    "top16:i32:9000:byte0:9", "top16:u32:9000:byte1:10", "top16:u32:3000:few:11", "top16:u32:5000:same:12",
+    "top16over:u32:30000:grp2:13", "top16over:i32:40001:grp2:14",
+    "top16s16:u32:9000:uniform:15", "top16s15:u32:9000:top8:16", "top16s14:u32:5000:few:17",
+    "top16s13:i32:20000:uniform:18", "top16s12:u32:20000:uniform:19",
+    # the region sample chooses: the top-16 path on a uniform input; the LSD
+    # passes in the same launches for oversized segments (two top-byte values,
+    # small keys, Zipf ranks), with a region overflow on byte 0, or with every
+    # digit constant
+    "top16auto:u32:20000:uniform:20", "top16auto_lsd:u32:20000:top8:21", "top16auto_lsd:u32:9000:low12:22",
+    "top16auto_lsd:i32:9000:zipf:23", "top16auto_lsdover:u32:30000:top8grp0:24",
+    "top16auto_lsdover:u32:20000:same:25",
+]
+
+
+def test_emulated_top16_path(emulator):
+    """Keys-only u32/i32 sorts on the top-16 launch sequence (region sample,
+    fused pass, its re-scatter launch, digit passes, local sort): small
+    tiles and blocks; production tiles; look-back groups of two tiles."""
+    run_cases("small", TOP16_SMALL, timeout=900)
+    run_cases("prod", ["top16:u32:300000:uniform:1", "top16:i32:100000:few:2", "top16over:u32:450000:grp2:3",
+                       "top16auto_lsd:u32:200000:top8:4"], timeout=900)
+    run_cases("groups", ["top16:u32:70000:uniform:1", "top16over:i32:30000:grp2:2"], env={"EMU_CUS": "8"})

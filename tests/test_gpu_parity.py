@@ -379,8 +379,10 @@ TOP16_CASES = [
     # a region of the fused pass overflows (byte 2 crowded into region
     # group 0): its second launch re-scatters into exact regions
     (2_000_000, "grp2", 4), (17_000_000, "grp2", 4),
-    # every digit constant: no pass after the fused one
-    (100_003, "same", 2),
+    # every key equal, forced onto the top-16 path (its fused pass counts
+    # digit 3 only, so it cannot see the constant digits): one segment of
+    # every key, sorted by its block a digit at a time
+    (100_003, "same", 3),
 ]
 
 
@@ -402,6 +404,19 @@ def test_top16_path(sorter, kind, n, dist, expect):
         assert sorter.first_pass() in expect
     finally:
         sorter.set_test_option(TEST_TOP16, TOP16_BY_SIZE)
+
+
+@pytest.mark.parametrize("dist,expect", [("uniform", (3,)), ("lowbits", (1,)), ("top8", (1,)), ("zipf", (1, 2)),
+                                         ("same", (2,))])
+def test_top16_sample_chooses(sorter, dist, expect):
+    """By size (2^25 + 7 u32 keys) the region sample chooses: the top-16
+    path for a uniform input; the LSD passes in the same launches when it
+    sees oversized segments (keys below 2^12, two top-byte values, Zipf ranks
+    below 2^20, whose lowest byte may overflow a region: re-scattered); no
+    pass after the fused one when every digit is constant."""
+    keys = make_keys("u32", (1 << 25) + 7, dist, seed=975)
+    check_buffer(sorter, "u32", keys)
+    assert sorter.first_pass() in expect
 
 
 @pytest.mark.parametrize("bits", [8, 11, 12, 13, 14, 15, 16])
