@@ -41,11 +41,11 @@ const char* const kKernelNames[] = {
     "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
     "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
-    "fs_local_k32",
+    "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_onesweep_loop_k32",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
-    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_COUNT
+    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_COUNT
 };
 
 }  // namespace
@@ -505,17 +505,23 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
 #ifdef FS_FAULT_INJECTION
         if (s->fault == FS_FAULT_EXTRA_BLOCK) grid += 1u;
 #endif
-        for (uint32_t l = 0; l < 2; ++l) {
-            uint32_t which = l;
-            void* argsf[] = {&a, &which};
-            if ((r = launch(s, key64(t) ? K_FIRST64 : K_FIRST32, l ? num_tiles : grid, s->block[var], argsf, st,
-                            no_alloc)) != FS_OK)
-                return r;
-        }
+        // a small grid for the launches that usually have nothing to do (one
+        // block per CU: the loop kernels' occupancy), so that they cost a few
+        // blocks instead of one per tile
+        const unsigned small = num_tiles < (uint32_t)s->num_cus ? num_tiles : (unsigned)s->num_cus;
+        if ((r = launch(s, key64(t) ? K_FIRST64 : K_FIRST32, grid, s->block[var], args1, st, no_alloc)) != FS_OK)
+            return r;
+        if ((r = launch(s, key64(t) ? K_RESCATTER64 : K_RESCATTER32, small, s->block[var], args1, st, no_alloc)) != FS_OK)
+            return r;
         for (uint32_t sl = 0; sl + 1 < a.digits; ++sl) {
             uint32_t slot = sl;
             void* args2[] = {&a, &slot};
-            if ((r = launch(s, K_OS32 + var, num_tiles, s->block[var], args2, st, no_alloc)) != FS_OK) return r;
+            // top-16 launch sequence: slot 0 is the digit-3 pass, or on the
+            // LSD passes the first of three; slots 1-2 run only for those
+            const bool loop = top16 && sl > 0;
+            if ((r = launch(s, loop ? K_LOOP32 : K_OS32 + var, loop ? small : num_tiles, s->block[var], args2, st,
+                            no_alloc)) != FS_OK)
+                return r;
         }
         if (top16 && (r = launch(s, K_LOCAL32, 1u << a.seg_bits, s->local_block, args1, st, no_alloc)) != FS_OK)
             return r;

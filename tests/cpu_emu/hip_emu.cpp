@@ -310,9 +310,12 @@ void fs_onesweep_k64(FsArgs, uint32_t);
 void fs_onesweep_k64_v(FsArgs, uint32_t);
 void fs_onesweep_any_k32(FsArgs, uint32_t);
 void fs_onesweep_any_k64(FsArgs, uint32_t);
-void fs_first_k32(FsArgs, uint32_t);
-void fs_first_k64(FsArgs, uint32_t);
+void fs_first_k32(FsArgs);
+void fs_first_k64(FsArgs);
 void fs_local_k32(FsArgs);
+void fs_rescatter_k32(FsArgs);
+void fs_rescatter_k64(FsArgs);
+void fs_onesweep_loop_k32(FsArgs, uint32_t);
 void fs_region_sample_k32(FsArgs);
 void fs_region_sample_k64(FsArgs);
 void fs_iota(uint32_t*, uint64_t);
@@ -339,9 +342,12 @@ static emu_function g_funcs[] = {
     {"fs_onesweep_k64_v", [](void** p) { fs_onesweep_k64_v(A0, D1); }},
     {"fs_onesweep_any_k32", [](void** p) { fs_onesweep_any_k32(A0, D1); }},
     {"fs_onesweep_any_k64", [](void** p) { fs_onesweep_any_k64(A0, D1); }},
-    {"fs_first_k32", [](void** p) { fs_first_k32(A0, D1); }},
-    {"fs_first_k64", [](void** p) { fs_first_k64(A0, D1); }},
+    {"fs_first_k32", [](void** p) { fs_first_k32(A0); }},
+    {"fs_first_k64", [](void** p) { fs_first_k64(A0); }},
     {"fs_local_k32", [](void** p) { fs_local_k32(A0); }},
+    {"fs_rescatter_k32", [](void** p) { fs_rescatter_k32(A0); }},
+    {"fs_rescatter_k64", [](void** p) { fs_rescatter_k64(A0); }},
+    {"fs_onesweep_loop_k32", [](void** p) { fs_onesweep_loop_k32(A0, D1); }},
     {"fs_region_sample_k32", [](void** p) { fs_region_sample_k32(A0); }},
     {"fs_region_sample_k64", [](void** p) { fs_region_sample_k64(A0); }},
     {"fs_iota", [](void** p) { fs_iota(*(uint32_t**)p[0], *(uint64_t*)p[1]); }},
