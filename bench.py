@@ -34,7 +34,10 @@ Prints one JSON line.  --gpus > 1 is refused: this build measures one GPU.
 --workload picks one of the other BASELINE.json configs (64-bit keys, floats,
 argsort, pairs, the 1M and 16M sizes) for the same measurement: its own metric
 line with the roofline of its dominant digit-pass kernel, no CPU baseline and
-no slice API.  The default (no flag) is the headline line above.
+no slice API.  The default (no flag) is the headline line above.  --path lsd
+or --path top16 forces the keys-only u32/i32 sort onto one of its two paths
+(the LSD digit passes; the top-16 path wherever its sample accepts the input),
+for profiling a path at a size where the library would pick the other one.
 """
 import argparse
 import ctypes
@@ -244,6 +247,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-slice-api", action="store_true")
+    ap.add_argument("--path", choices=("auto", "lsd", "top16"), default="auto",
+                    help="keys-only u32/i32 sorts: the library's choice (auto), the LSD digit passes at any "
+                         "size (lsd), or the top-16 path wherever its sample accepts the input (top16)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -258,8 +264,11 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
 
+    if args.path != "auto":
+        from forge_sort import TEST_TOP16, TOP16_NEVER, TOP16_SAMPLED
+        sorter.set_test_option(TEST_TOP16, TOP16_NEVER if args.path == "lsd" else TOP16_SAMPLED)
     wl = args.workload
-    headline = wl == "u32_256M"
+    headline = wl == "u32_256M" and args.path == "auto"
     op_name, kind, n_default, data_desc, cfg_ref = WORKLOADS[wl]
     n = args.n or n_default
     K, W = args.steps, args.warmup
@@ -414,13 +423,15 @@ def main():
         workload = "sort_buffer u32, 268,435,456 keys, device resident (BASELINE.json configs[1])"
     else:
         workload = f"{api} {kind}, {n:,} keys, device resident (BASELINE.json {cfg_ref})"
+        if args.path != "auto":
+            workload += f", path forced: {args.path}"
     line = {
         "metric": METRIC if headline else f"Mkeys/s ({wl}, 1 MI355X) and % of HBM-bandwidth roofline",
         "value": round(value, 1), "unit": "Mkeys/s", "n_gpus": 1,
         "steps": K, "warmup": W, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": kind,
         "data": f"synthetic: {data_desc}, resident in HBM",
-        "config": {"workload": workload, "n": n, "key_type": kind, "op": api},
+        "config": {"workload": workload, "n": n, "key_type": kind, "op": api, "path": args.path},
         "roofline": roofline,
         "sort_roofline": {"bytes_per_key": sort_bytes, "frac": round(sort_frac, 4),
                           "achieved_GBps": round(sort_frac * HBM_PEAK_GBS, 1)},
