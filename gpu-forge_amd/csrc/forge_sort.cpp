@@ -41,11 +41,11 @@ const char* const kKernelNames[] = {
     "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
     "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
-    "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_onesweep_loop_k32",
+    "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_onesweep_loop_k32", "fs_local_k64",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
-    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_COUNT
+    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_LOCAL64, K_COUNT
 };
 
 }  // namespace
@@ -58,8 +58,8 @@ struct fs_sorter {
     hipFunction_t fn[K_COUNT] = {};
     uint32_t tile[4] = {};          // keys per tile of each digit-pass variant (FS_VAR_*)
     uint32_t block[4] = {};         // threads per block of each variant
-    uint32_t local_keys = 0;        // keys a block of the local sort holds (fs_local_k32)
-    uint32_t local_block = 0;       // its threads per block
+    uint32_t local_keys[2] = {};    // keys a block of the local sort holds (fs_local_k32, fs_local_k64)
+    uint32_t local_block[2] = {};   // their threads per block
     int num_cus = 256;
 
     DevBuf s1k, s2k, s1v, s2v, lb0, lb1, iok, iov, tilemap;
@@ -312,20 +312,28 @@ static bool fused_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
     return s->fused_mode == 2u || n >= FS_FUSED_MIN_KEYS;
 }
 
-// Keys-only u32/i32 sorts from FS_TOP16_MIN_KEYS keys take the top-16 path
-// (fused pass on digit 2, stable pass on digit 3, local sort of each
-// segment); it needs the fused pass's regions, hence the fused range.
+// Keys a block of the local sort holds for keys of this type.
+static uint32_t local_keys_of(const fs_sorter* s, fs_key_type t) { return s->local_keys[key64(t) ? 1 : 0]; }
+
+// Keys-only integer sorts (u32, i32, u64, i64) from FS_TOP16_MIN_KEYS keys
+// take the top-16 path (fused pass on the digit below the top byte, stable
+// pass on the top digit, local sort of each segment); it needs the fused
+// pass's regions, hence the fused range.  Float keys keep the LSD passes:
+// their top 16 bits (sign, exponent, a few mantissa bits) are concentrated
+// in a few values for most data, which the region sample would refuse.
 static bool top16_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
-    if (op != FS_OP_SORT || (t != FS_KEY_U32 && t != FS_KEY_I32) || s->top16_mode == 1u || n < 2) return false;
+    if (op != FS_OP_SORT || s->top16_mode == 1u || n < 2) return false;
+    if (t != FS_KEY_U32 && t != FS_KEY_I32 && t != FS_KEY_U64 && t != FS_KEY_I64) return false;
     if (n > (1ull << 31) || s->fused_mode == 1u) return false;
-    if (FS_FUSED_S1_KEYS(fused_sub_keys(n, s->tile[FS_VAR_K32])) >= (1ull << 32)) return false;
+    if (FS_FUSED_S1_KEYS(fused_sub_keys(n, s->tile[variant_of(op, t)])) >= (1ull << 32)) return false;
     if (s->top16_mode >= 2u) return true;
     // By size: the 2^16 segments of a uniform input must fit a block with a
     // margin of five standard deviations (local_keys - 5 sqrt(local_keys)
     // keys each on average), so that hardly any takes the big-segment path.
+    const uint64_t lk = local_keys_of(s, t);
     uint64_t root = 0;
-    while ((root + 1) * (root + 1) <= s->local_keys) ++root;
-    const uint64_t mean_max = s->local_keys > 5 * root ? s->local_keys - 5 * root : 0;
+    while ((root + 1) * (root + 1) <= lk) ++root;
+    const uint64_t mean_max = lk > 5 * root ? lk - 5 * root : 0;
     return n >= FS_TOP16_MIN_KEYS && n <= (mean_max << 16);
 }
 
@@ -480,10 +488,10 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.sub_keys = fused ? (uint32_t)sub_keys : 0u;
     a.s1_keys = fused ? (uint32_t)FS_FUSED_S1_KEYS(sub_keys) : 0u;
     a.segc = top16 ? sc.segc : 0u;
-    a.seg_bits = top16 ? (s->seg_bits ? s->seg_bits : seg_bits_for(n, s->local_keys)) : 0u;
+    a.seg_bits = top16 ? (s->seg_bits ? s->seg_bits : seg_bits_for(n, local_keys_of(s, t))) : 0u;
     // a segment the region sample estimates above 16 blocks' keys sends the
     // sort to the LSD passes (unless a test forces the top-16 path)
-    a.seg_limit = s->top16_mode == 2u ? 0xFFFFFFFFu : 16u * s->local_keys;
+    a.seg_limit = s->top16_mode == 2u ? 0xFFFFFFFFu : 16u * local_keys_of(s, t);
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 #ifdef FS_FAULT_INJECTION
@@ -516,14 +524,17 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         for (uint32_t sl = 0; sl + 1 < a.digits; ++sl) {
             uint32_t slot = sl;
             void* args2[] = {&a, &slot};
-            // top-16 launch sequence: slot 0 is the digit-3 pass, or on the
-            // LSD passes the first of three; slots 1-2 run only for those
-            const bool loop = top16 && sl > 0;
+            // top-16 launch sequence: slot 0 is the top digit's pass, or on
+            // the LSD passes the first of them; the other slots run only for
+            // those (32-bit keys: the loop kernel's small grid; 64-bit keys
+            // keep one block per tile: the loop kernel spills there)
+            const bool loop = top16 && sl > 0 && !key64(t);
             if ((r = launch(s, loop ? K_LOOP32 : K_OS32 + var, loop ? small : num_tiles, s->block[var], args2, st,
                             no_alloc)) != FS_OK)
                 return r;
         }
-        if (top16 && (r = launch(s, K_LOCAL32, 1u << a.seg_bits, s->local_block, args1, st, no_alloc)) != FS_OK)
+        if (top16 && (r = launch(s, key64(t) ? K_LOCAL64 : K_LOCAL32, 1u << a.seg_bits, s->local_block[key64(t) ? 1 : 0],
+                                 args1, st, no_alloc)) != FS_OK)
             return r;
         s->last_stream = st;
         s->pending = true;
@@ -658,12 +669,15 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
                 return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object has an invalid tile geometry");
         hipDeviceptr_t lp = nullptr;
         size_t lsz = 0;
-        uint32_t lg[2] = {0, 0};
-        if (hipModuleGetGlobal(&lp, &lsz, s->module, "fs_kernel_local_geometry") != hipSuccess || lsz != 8 ||
-            hipMemcpyDtoH(lg, lp, 8) != hipSuccess || lg[0] == 0 || lg[1] < FS_RADIX)
+        uint32_t lg[4] = {0, 0, 0, 0};
+        if (hipModuleGetGlobal(&lp, &lsz, s->module, "fs_kernel_local_geometry") != hipSuccess || lsz != 16 ||
+            hipMemcpyDtoH(lg, lp, 16) != hipSuccess || lg[0] == 0 || lg[1] < FS_RADIX || lg[2] == 0 ||
+            lg[3] < FS_RADIX)
             return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object lacks a valid fs_kernel_local_geometry");
-        s->local_keys = lg[0];
-        s->local_block = lg[1];
+        for (int i = 0; i < 2; ++i) {
+            s->local_keys[i] = lg[2 * i];
+            s->local_block[i] = lg[2 * i + 1];
+        }
     }
     const size_t tab = (size_t)FS_MAX_DIGITS * FS_RADIX * 4;
     if (hipMalloc(&s->hist, (size_t)FS_HIST_WORDS * 4) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||

@@ -233,8 +233,8 @@
 #define FS_PLAN_NPASSES (FS_MAX_DIGITS * FS_PLAN_PASS_WORDS)      // passes that run
 #define FS_PLAN_MASK (FS_PLAN_NPASSES + 1)                         // bit j: digit j sorted
 #define FS_MASK_FUSED (1u << 8)     // mask word: the fused first pass's regions were used
-#define FS_MASK_TOP16 (1u << 9)     // mask word: the top-16 path ran (digit passes on digits 2 and 3,
-                                    // then the local sort of each top-16-bit segment)
+#define FS_MASK_TOP16 (1u << 9)     // mask word: the top-16 path ran (digit passes on the two top
+                                    // digits, then the local sort of each top-16-bit segment)
 #define FS_PLAN_TICKET (FS_PLAN_NPASSES + 2)                       // upsweep blocks finished (0 between sorts)
 // Local sort of the top-16 path (fs_local_*): word FS_PLAN_LOCAL = active | seg_bits << 8 |
 // flags << 16, word FS_PLAN_LOCAL + 1 = buffer ids as a pass's word 2j+1.
@@ -244,21 +244,22 @@
 #define FS_PLAN_RESCATTER (FS_PLAN_NPASSES + 6)
 #define FS_PLAN_WORDS (FS_PLAN_NPASSES + 8)
 
-// Top-16 path of keys-only 32-bit sorts (from FS_TOP16_MIN_KEYS keys): the
-// fused first pass scatters by digit 2 (the region sample's choice,
-// FS_RTABLE_SDIGIT) into its regions, a
-// stable pass on digit 3 reads the regions in digit-2 order - so its output is
-// ordered by the top 16 bits - and counts the keys of every top-16-bit value
-// (FS_SEGS counters), and the local sort (fs_local_*) sorts each segment of
-// keys sharing their top seg_bits bits, in LDS, by the bits below: one block
-// per segment, one read and one write of every key.  A segment larger than a
-// block holds is sorted by that block through scratch, a digit at a time.
+// Top-16 path of keys-only integer sorts (from FS_TOP16_MIN_KEYS keys): the
+// fused first pass scatters by the digit below the top byte (digit 2 of
+// 32-bit keys, 6 of 64-bit keys; the region sample's choice,
+// FS_RTABLE_SDIGIT) into its regions, a stable pass on the top digit reads
+// the regions in order - so its output is ordered by the top 16 bits - and
+// counts the keys of every top-16-bit value (FS_SEGS counters), and the
+// local sort (fs_local_*) sorts each segment of keys sharing their top
+// seg_bits bits, in LDS, by the bits below: one block per segment, one read
+// and one write of every key.  A segment larger than a block holds is sorted
+// by that block through scratch, a digit at a time.
 // seg_bits is chosen on the host so that a segment of a uniform input fits
 // a block.  The region sample estimates the segments from its keys (their
 // top seg_bits bits): one estimated above FsArgs.seg_limit keys (skewed or
 // constant top bytes) makes it choose digit 0 instead, and the same launches
-// run the LSD passes (the stable passes on digits 1-3 in the digit-pass
-// launches, the local sort's launch idle).
+// run the LSD passes (the stable passes on the other digits in the
+// digit-pass launches, the local sort's launch idle).
 #define FS_SEGS 65536u
 // a segment estimate counts only from this many sampled keys on
 #define FS_SEG_MIN_SAMPLES 8u
@@ -267,6 +268,22 @@
 #endif
 #ifndef FS_L32_ITEMS
 #define FS_L32_ITEMS 18
+#endif
+// 64-bit keys: 256 x 10 keys per block (a 20 KiB stage: five blocks per CU)
+#ifndef FS_L64_BLOCK
+#define FS_L64_BLOCK 256
+#endif
+#ifndef FS_L64_ITEMS
+#define FS_L64_ITEMS 10
+#endif
+// ... grouped by the FS_L64_GBITS bits below the segment's (2^11 LDS
+// counters: about one key per group), each key then ranked within its group
+// by comparison when no group holds more than FS_L64_GLIM keys
+#ifndef FS_L64_GBITS
+#define FS_L64_GBITS 11
+#endif
+#ifndef FS_L64_GLIM
+#define FS_L64_GLIM 32u
 #endif
 
 // Error bits additionally reported through the status word.

@@ -313,6 +313,7 @@ void fs_onesweep_any_k64(FsArgs, uint32_t);
 void fs_first_k32(FsArgs);
 void fs_first_k64(FsArgs);
 void fs_local_k32(FsArgs);
+void fs_local_k64(FsArgs);
 void fs_rescatter_k32(FsArgs);
 void fs_rescatter_k64(FsArgs);
 void fs_onesweep_loop_k32(FsArgs, uint32_t);
@@ -323,7 +324,7 @@ void fs_scratch_address(uint64_t*);
 void fs_gather_elems(uint64_t, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint64_t);
 extern uint32_t fs_kernel_tile_keys[4];
 extern uint32_t fs_kernel_block_threads[4];
-extern uint32_t fs_kernel_local_geometry[2];
+extern uint32_t fs_kernel_local_geometry[4];
 }
 
 struct emu_function {
@@ -345,6 +346,7 @@ static emu_function g_funcs[] = {
     {"fs_first_k32", [](void** p) { fs_first_k32(A0); }},
     {"fs_first_k64", [](void** p) { fs_first_k64(A0); }},
     {"fs_local_k32", [](void** p) { fs_local_k32(A0); }},
+    {"fs_local_k64", [](void** p) { fs_local_k64(A0); }},
     {"fs_rescatter_k32", [](void** p) { fs_rescatter_k32(A0); }},
     {"fs_rescatter_k64", [](void** p) { fs_rescatter_k64(A0); }},
     {"fs_onesweep_loop_k32", [](void** p) { fs_onesweep_loop_k32(A0, D1); }},

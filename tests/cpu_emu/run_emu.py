@@ -64,21 +64,25 @@ def keys_for(kind, n, dist, seed, tile=None):
         in0 = (np.arange(n) // tile // 8) % 8 == 0
         b[in0] = (b[in0] & ~BITS[kind](0xFF)) | BITS[kind](3)
     elif dist == "grp2":
-        # byte 2 is 3 in the tiles of region group 0 (as grp0, for the top-16
-        # path's fused pass, which scatters by byte 2)
+        # the byte below the top byte (2, or 6 for 64-bit keys) is 3 in the
+        # tiles of region group 0 (as grp0, for the top-16 path's fused pass,
+        # which scatters by that byte)
         b = g.integers(0, 1 << (64 if wide else 32), size=n, dtype=BITS[kind], endpoint=False)
         in0 = (np.arange(n) // tile // 8) % 8 == 0
-        b[in0] = (b[in0] & ~BITS[kind](0xFF0000)) | BITS[kind](0x30000)
+        sh = BITS[kind](48 if wide else 16)
+        b[in0] = (b[in0] & ~(BITS[kind](0xFF) << sh)) | (BITS[kind](3) << sh)
     elif dist == "top8":
         # the top byte only two values: segments of the local sort far larger
         # than a block holds
-        b = g.integers(0, 1 << 24, size=n, dtype=BITS[kind])
-        b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](24)
+        top = 56 if wide else 24
+        b = g.integers(0, 1 << top, size=n, dtype=BITS[kind])
+        b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](top)
     elif dist == "top8grp0":
         # two top-byte values (the top-16 sequence's sample takes the LSD
         # passes) and byte 0 crowded into region group 0 (its region overflows)
-        b = g.integers(0, 1 << 24, size=n, dtype=BITS[kind])
-        b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](24)
+        top = 56 if wide else 24
+        b = g.integers(0, 1 << top, size=n, dtype=BITS[kind])
+        b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](top)
         in0 = (np.arange(n) // tile // 8) % 8 == 0
         b[in0] = (b[in0] & ~BITS[kind](0xFF)) | BITS[kind](3)
     elif dist == "zipf":

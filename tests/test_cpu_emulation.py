@@ -242,14 +242,23 @@ TOP16_SMALL = [
     "top16auto:u32:20000:uniform:20", "top16auto_lsd:u32:20000:top8:21", "top16auto_lsd:u32:9000:low12:22",
     "top16auto_lsd:i32:9000:zipf:23", "top16auto_lsdover:u32:30000:top8grp0:24",
     "top16auto_lsdover:u32:20000:same:25",
+    # 64-bit keys: the fused pass on byte 6, the stable pass on byte 7, the
+    # group sort of each segment; its LSD fallback in LDS (groups of equal
+    # keys above the comparison limit), the big-segment path, re-scatter
+    "top16:u64:5000:uniform:31", "top16:i64:9000:uniform:32", "top16:u64:2:uniform:33", "top16:i64:100:uniform:34",
+    "top16:u64:1500:few:35", "top16:u64:3000:few:36", "top16:u64:5000:same:37", "top16:u64:9000:top8:38",
+    "top16:u64:1025:low12:39", "top16:i64:9000:zipf:40", "top16over:u64:30000:grp2:41",
+    "top16s16:u64:9000:uniform:42", "top16s12:i64:20000:uniform:43",
+    "top16auto:u64:20000:uniform:44", "top16auto_lsd:u64:20000:top8:45", "top16auto_lsdover:i64:30000:top8grp0:46",
 ]
 
 
 def test_emulated_top16_path(emulator):
-    """Keys-only u32/i32 sorts on the top-16 launch sequence (region sample,
+    """Keys-only u32/i32/u64/i64 sorts on the top-16 launch sequence (region sample,
     fused pass, its re-scatter launch, digit passes, local sort): small
     tiles and blocks; production tiles; look-back groups of two tiles."""
     run_cases("small", TOP16_SMALL, timeout=900)
     run_cases("prod", ["top16:u32:300000:uniform:1", "top16:i32:100000:few:2", "top16over:u32:450000:grp2:3",
-                       "top16auto_lsd:u32:200000:top8:4"], timeout=900)
+                       "top16auto_lsd:u32:200000:top8:4", "top16:u64:200000:uniform:5", "top16:i64:60000:few:6",
+                       "top16over:u64:300000:grp2:7"], timeout=900)
     run_cases("groups", ["top16:u32:70000:uniform:1", "top16over:i32:30000:grp2:2"], env={"EMU_CUS": "8"})

@@ -137,13 +137,17 @@ def make_keys(kind, n, dist, seed, tile=None):
         b = g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False)
         in0 = (np.arange(n) // tile // 8) % 8 == 0
         b[in0] = (b[in0] & ~BITS[kind](0xFF)) | BITS[kind](3)
-    elif dist == "grp2":        # byte 2 is 3 in the tiles of region group 0 (the top-16 path's fused pass)
-        b = g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False)
+    elif dist == "grp2":        # the byte below the top one (2; 6 of 64-bit keys) is 3 in the tiles of
+        b = g.integers(0, hi, size=n, dtype=BITS[kind], endpoint=False)   # region group 0 (top-16 fused pass)
         in0 = (np.arange(n) // tile // 8) % 8 == 0
-        b[in0] = (b[in0] & ~BITS[kind](0xFF0000)) | BITS[kind](0x30000)
+        sh = BITS[kind](48 if wide else 16)
+        b[in0] = (b[in0] & ~(BITS[kind](0xFF) << sh)) | (BITS[kind](3) << sh)
     elif dist == "top8":        # the top byte only two values: segments far larger than a block holds
-        b = g.integers(0, 1 << 24, size=n, dtype=BITS[kind])
-        b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](24)
+        top = 56 if wide else 24
+        b = g.integers(0, 1 << top, size=n, dtype=BITS[kind])
+        b |= np.where(g.integers(0, 2, size=n) == 0, 0x10, 0xF0).astype(BITS[kind]) << BITS[kind](top)
+    elif dist == "dup":         # 2^16 distinct values: every key has ~n / 2^16 equal ones
+        b = g.choice(g.integers(0, hi, size=1 << 16, dtype=BITS[kind], endpoint=False), size=n)
     elif dist == "zipf":        # Zipf(1.1) ranks below 2^20: a few huge segments, many tiny ones
         b = np.minimum(g.zipf(1.1, size=n) - 1, (1 << 20) - 1).astype(BITS[kind])
     else:
@@ -406,6 +410,37 @@ def test_top16_path(sorter, kind, n, dist, expect):
         sorter.set_test_option(TEST_TOP16, TOP16_BY_SIZE)
 
 
+TOP16_CASES_64 = [
+    (2, "uniform", 3), (100, "uniform", 3), (4097, "uniform", 3), (1_000_003, "uniform", 3),
+    (16_777_216, "uniform", 3), (5_000_000, "sorted", (3, 4)), (3_000_001, "reverse", (3, 4)),
+    (300_007, "byte0", 3), (2_000_000, "lowbits", 3), (1_000_000, "few", 3), (2_000_003, "zipf", 3),
+    (3_000_000, "top8", 3), (2_000_000, "grp2", 4), (100_003, "same", 3),
+    # many equal keys per segment: groups above the comparison limit, each
+    # segment sorted by the LSD passes in LDS instead
+    (8_000_000, "dup", 3), (300_000, "dup", 3),
+]
+
+
+@pytest.mark.parametrize("kind", ["u64", "i64"])
+@pytest.mark.parametrize("n,dist,expect", TOP16_CASES_64)
+def test_top16_path_64(sorter, kind, n, dist, expect):
+    """Keys-only u64/i64 sorts on the top-16 path (fused pass on byte 6,
+    stable pass on byte 7 counting the segments, group sort of each
+    segment), forced at every size: exact against the oracle through the
+    slice and buffer APIs, and beginning the way the case names."""
+    from forge_sort import TEST_TOP16, TOP16_ALWAYS, TOP16_BY_SIZE
+    keys = make_keys(kind, n, dist, seed=990 + n % 89, tile=sorter.tile_config()["k64"])
+    sorter.set_test_option(TEST_TOP16, TOP16_ALWAYS)
+    try:
+        expect = expect if isinstance(expect, tuple) else (expect,)
+        check_sort(sorter, kind, keys)
+        assert sorter.first_pass() in expect
+        check_buffer(sorter, kind, keys)
+        assert sorter.first_pass() in expect
+    finally:
+        sorter.set_test_option(TEST_TOP16, TOP16_BY_SIZE)
+
+
 @pytest.mark.parametrize("dist,expect", [("uniform", (3,)), ("lowbits", (1,)), ("top8", (1,)), ("zipf", (1, 2)),
                                          ("same", (2,))])
 def test_top16_sample_chooses(sorter, dist, expect):
@@ -416,6 +451,21 @@ def test_top16_sample_chooses(sorter, dist, expect):
     pass after the fused one when every digit is constant."""
     keys = make_keys("u32", (1 << 25) + 7, dist, seed=975)
     check_buffer(sorter, "u32", keys)
+    assert sorter.first_pass() in expect
+
+
+@pytest.mark.parametrize("kind", ["u64", "i64", "f64"])
+@pytest.mark.parametrize("dist", ["uniform", "lowbits", "top8", "same"])
+def test_top16_sample_chooses_64(sorter, kind, dist):
+    """The same by size for 2^25 + 7 64-bit keys: u64/i64 uniform keys take
+    the top-16 path, the others the LSD passes in the same launches (none
+    after the fused pass for equal keys); f64 keys always the fused LSD
+    passes (float keys do not take the top-16 launch sequence)."""
+    keys = make_keys(kind, (1 << 25) + 7, dist, seed=976)
+    check_buffer(sorter, kind, keys)
+    expect = {"uniform": (3,), "lowbits": (1,), "top8": (1,), "same": (2,)}[dist]
+    if kind == "f64":
+        expect = (1, 2)
     assert sorter.first_pass() in expect
 
 
