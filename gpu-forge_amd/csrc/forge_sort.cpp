@@ -42,10 +42,11 @@ const char* const kKernelNames[] = {
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
     "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
     "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_onesweep_loop_k32", "fs_local_k64",
+    "fs_local_deferred_k64",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
-    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_LOCAL64, K_COUNT
+    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_LOCAL64, K_DEFER64, K_COUNT
 };
 
 }  // namespace
@@ -69,7 +70,7 @@ struct fs_sorter {
     uint32_t* rstart = nullptr;     // [FS_REGIONS + 1] region starts
     uint32_t* rtable = nullptr;     // [FS_RTABLE_WORDS] region bases, total and caps of the fused pass
     uint32_t* plan = nullptr;       // u32[FS_PLAN_WORDS] device-side schedule
-    uint32_t* segc = nullptr;       // u32[FS_SEGS] segment counters of the top-16 path
+    uint32_t* segc = nullptr;       // u32[FS_SEGC_WORDS] segment counters and deferred-segment list of the top-16 path
     uint32_t* status = nullptr;     // pinned host word written by kernels on device errors
     unsigned long long* stats = nullptr;   // device u64[FS_STAT_COUNT]
     bool stats_on = false;
@@ -536,6 +537,10 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         if (top16 && (r = launch(s, key64(t) ? K_LOCAL64 : K_LOCAL32, 1u << a.seg_bits, s->local_block[key64(t) ? 1 : 0],
                                  args1, st, no_alloc)) != FS_OK)
             return r;
+        // 64-bit keys: the segments the local sort deferred (larger than a
+        // block, or many equal keys), on a small grid
+        if (top16 && key64(t) && (r = launch(s, K_DEFER64, small, s->local_block[1], args1, st, no_alloc)) != FS_OK)
+            return r;
         s->last_stream = st;
         s->pending = true;
         s->last_plan = (uint32_t*)(uintptr_t)sc.plan;
@@ -684,7 +689,7 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
         hipMalloc(&s->cursors, FS_REGIONS * 4) != hipSuccess || hipMalloc(&s->rstart, (FS_REGIONS + 1) * 4) != hipSuccess ||
         hipMalloc(&s->rtable, FS_RTABLE_WORDS * 4) != hipSuccess ||
         hipMalloc(&s->plan, FS_PLAN_WORDS * sizeof(uint32_t)) != hipSuccess ||
-        hipMalloc(&s->segc, FS_SEGS * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc(&s->segc, FS_SEGC_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc(&s->stats, FS_STAT_SLOTS * FS_STAT_COUNT * sizeof(unsigned long long)) != hipSuccess ||
         hipHostMalloc(&s->status, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
         return create_failed(s, FS_ERR_OUT_OF_MEMORY, "device tables of the sorter");

@@ -261,6 +261,9 @@
 // run the LSD passes (the stable passes on the other digits in the
 // digit-pass launches, the local sort's launch idle).
 #define FS_SEGS 65536u
+// the segment counters, a count (zero before the local sort) and a list of
+// segment ids (the 64-bit local sort's deferred segments)
+#define FS_SEGC_WORDS (2u * FS_SEGS + 1u)
 // a segment estimate counts only from this many sampled keys on
 #define FS_SEG_MIN_SAMPLES 8u
 #ifndef FS_L32_BLOCK
@@ -269,12 +272,12 @@
 #ifndef FS_L32_ITEMS
 #define FS_L32_ITEMS 18
 #endif
-// 64-bit keys: 256 x 10 keys per block (a 20 KiB stage: five blocks per CU)
+// 64-bit keys: 256 x 9 keys per block (an 18 KiB stage: five blocks per CU)
 #ifndef FS_L64_BLOCK
 #define FS_L64_BLOCK 256
 #endif
 #ifndef FS_L64_ITEMS
-#define FS_L64_ITEMS 10
+#define FS_L64_ITEMS 9
 #endif
 // ... grouped by the FS_L64_GBITS bits below the segment's (2^11 LDS
 // counters: about one key per group), each key then ranked within its group
@@ -367,7 +370,9 @@ typedef struct FsArgs {
     uint32_t s1_keys;           // keys S1 holds (fused path: the regions' budget), else 0
     uint32_t seg_limit;         // top-16 path: the region sample takes the LSD passes instead when it
                                 // estimates a segment of more keys than this (0xFFFFFFFF: never)
-    uint64_t segc;              // u32[FS_SEGS] keys per top-16-bit value (top-16 path; zero before its digit-3 pass)
+    uint64_t segc;              // u32[FS_SEGC_WORDS]: keys per top-16-bit value (top-16 path; zero before its
+                                // top-digit pass), then the count and list of the segments the 64-bit local
+                                // sort leaves to its second launch
     uint32_t seg_bits;          // top-16 launch sequence: bits that name a segment of the local sort
                                 // (8..16), else 0
     uint32_t reserved0;

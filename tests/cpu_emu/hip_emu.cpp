@@ -314,6 +314,7 @@ void fs_first_k32(FsArgs);
 void fs_first_k64(FsArgs);
 void fs_local_k32(FsArgs);
 void fs_local_k64(FsArgs);
+void fs_local_deferred_k64(FsArgs);
 void fs_rescatter_k32(FsArgs);
 void fs_rescatter_k64(FsArgs);
 void fs_onesweep_loop_k32(FsArgs, uint32_t);
@@ -347,6 +348,7 @@ static emu_function g_funcs[] = {
     {"fs_first_k64", [](void** p) { fs_first_k64(A0); }},
     {"fs_local_k32", [](void** p) { fs_local_k32(A0); }},
     {"fs_local_k64", [](void** p) { fs_local_k64(A0); }},
+    {"fs_local_deferred_k64", [](void** p) { fs_local_deferred_k64(A0); }},
     {"fs_rescatter_k32", [](void** p) { fs_rescatter_k32(A0); }},
     {"fs_rescatter_k64", [](void** p) { fs_rescatter_k64(A0); }},
     {"fs_onesweep_loop_k32", [](void** p) { fs_onesweep_loop_k32(A0, D1); }},

@@ -1,0 +1,144 @@
+"""Performance guards, after the reference's perf-test suite
+(metal-forge-compute/forge-sort/tests/performance.rs:37-207): 16,000,000 keys
+per type, one warm-up call, the median of 10 timed calls, a floor in Mkeys/s.
+
+Two sets:
+* the reference's own cases and floors, through the same host-slice API
+  (copy in, sort, copy out: bound by the host link, not by the kernels);
+  inputs from numpy's PCG64 with the reference's seeds (its ChaCha8 stream is
+  a Rust crate's and is not available here), the same value ranges;
+* the same cases on device-resident buffers (sort_<t>_buffer, argsort and
+  pairs on device pointers), the path the kernels set, with floors at about
+  half the rates measured on MI355X, so that a regression of the kernels,
+  and not of the host link, fails them.
+"""
+import time
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+N = 16_000_000
+REPS = 10
+
+
+@pytest.fixture(scope="module")
+def sorter():
+    from forge_sort import GpuSorter
+    s = GpuSorter.new()
+    yield s
+    s.close()
+
+
+def rng(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def keys_for(kind, seed):
+    g = rng(seed)
+    if kind in ("u32", "i32", "u64", "i64"):
+        bits = np.uint32 if kind.endswith("32") else np.uint64
+        b = g.integers(0, 1 << (8 * np.dtype(bits).itemsize), size=N, dtype=bits, endpoint=False)
+        return b.view(np.int32 if kind == "i32" else np.int64 if kind == "i64" else bits)
+    dt = np.float32 if kind == "f32" else np.float64
+    return (g.random(N, dtype=dt) * dt(2000.0) - dt(1000.0)).astype(dt)   # rng.gen::<f>() * 2000 - 1000
+
+
+def median_mkeys(run, prepare=None):
+    """Mkeys/s of the median of REPS timed calls of run() (prepare() before
+    each, untimed), after one warm-up call."""
+    if prepare:
+        prepare()
+    run()
+    times = []
+    for _ in range(REPS):
+        if prepare:
+            prepare()
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return N / float(np.median(times)) / 1e6
+
+
+# (case, seed, floor in Mkeys/s): performance.rs:37-207
+SLICE_CASES = [("sort_u32", 42, 2000.0), ("sort_i32", 43, 1900.0), ("sort_f32", 44, 500.0),
+               ("argsort_u32", 45, 750.0), ("sort_pairs_f32", 46, 250.0), ("sort_u64", 47, 600.0),
+               ("sort_i64", 48, 550.0), ("sort_f64", 49, 100.0)]
+
+
+@pytest.mark.parametrize("case,seed,floor", SLICE_CASES)
+def test_perf_slice(sorter, case, seed, floor):
+    """The reference's perf tests and floors, host-slice API (performance.rs:37-207)."""
+    kind = case.split("_")[-1]
+    keys = keys_for(kind, seed)
+    if case.startswith("argsort"):
+        mks = median_mkeys(lambda: sorter.argsort_u32(keys))
+    elif case.startswith("sort_pairs"):
+        vals0 = rng(seed + 1000).integers(0, 1 << 32, size=N, dtype=np.uint32)
+        work = {}
+
+        def prep():
+            work["k"], work["v"] = keys.copy(), vals0.copy()
+        mks = median_mkeys(lambda: sorter.sort_pairs_f32(work["k"], work["v"]), prep)
+    else:
+        work = {}
+
+        def prep():
+            work["k"] = keys.copy()
+        mks = median_mkeys(lambda: getattr(sorter, case)(work["k"]), prep)
+    print(f"{case} slice 16M: {mks:,.0f} Mkeys/s (floor {floor:,.0f})")
+    assert mks >= floor, f"{case}: {mks:,.0f} Mkeys/s < {floor:,.0f}"
+
+
+# (case, seed, floor in Mkeys/s): device-resident, floors about half the
+# rates measured on one MI355X
+DEVICE_CASES = [("sort_u32", 42, 35000.0), ("sort_i32", 43, 35000.0), ("sort_f32", 44, 30000.0),
+                ("argsort_u32", 45, 25000.0), ("sort_pairs_f32", 46, 20000.0), ("sort_u64", 47, 10000.0),
+                ("sort_i64", 48, 10000.0), ("sort_f64", 49, 10000.0)]
+
+
+@pytest.mark.parametrize("case,seed,floor", DEVICE_CASES)
+def test_perf_device(sorter, case, seed, floor):
+    """The same cases on device-resident buffers (no host copies timed)."""
+    kind = case.split("_")[-1]
+    keys = keys_for(kind, seed)
+    ksz = keys.dtype.itemsize
+    src = sorter.alloc_sort_buffer(kind, N)
+    src.copy_from_slice(keys)
+    work = sorter.alloc_sort_buffer(kind, N)
+    extra = []
+    try:
+        def copy_keys():
+            sorter.copy_device(work.device_ptr(), src.device_ptr(), ksz * N)
+            sorter.device_synchronize()
+        if case.startswith("argsort"):
+            idx = sorter.alloc_sort_buffer("u32", N)
+            extra.append(idx)
+            mks = median_mkeys(lambda: sorter.argsort_device(kind, work.device_ptr(), N, idx.device_ptr()),
+                               copy_keys)
+        elif case.startswith("sort_pairs"):
+            vsrc = sorter.alloc_sort_buffer("u32", N)
+            vsrc.copy_from_slice(rng(seed + 1000).integers(0, 1 << 32, size=N, dtype=np.uint32))
+            vals = sorter.alloc_sort_buffer("u32", N)
+            extra += [vsrc, vals]
+
+            def copy_both():
+                sorter.copy_device(vals.device_ptr(), vsrc.device_ptr(), 4 * N)
+                copy_keys()
+            mks = median_mkeys(lambda: sorter.sort_pairs_device(kind, work.device_ptr(), vals.device_ptr(), N),
+                               copy_both)
+        else:
+            mks = median_mkeys(lambda: sorter.sort_device(kind, work.device_ptr(), N), copy_keys)
+        work.set_len(N)                                  # (filled by device copies, not copy_from_slice)
+        out = work.as_slice()
+        exp = np.sort(keys)                              # (no NaN in these inputs)
+        if not case.startswith("argsort"):
+            assert np.array_equal(out, exp), f"{case}: output differs from numpy's sort"
+    finally:
+        for b in extra:
+            b.free()
+        work.free()
+        src.free()
+    print(f"{case} device 16M: {mks:,.0f} Mkeys/s (floor {floor:,.0f})")
+    assert mks >= floor, f"{case}: {mks:,.0f} Mkeys/s < {floor:,.0f}"
