@@ -68,7 +68,21 @@ typedef struct fs_sorter fs_sorter;
 fs_status fs_sorter_new(int device, fs_sorter **out);
 
 /* GpuSorter::with_context (lib.rs:606-686).  Uses the caller's HIP stream
- * (`hip_stream`, not owned; NULL = the default stream) on `device`. */
+ * (`hip_stream`, not owned; NULL = the default stream) on `device`.
+ *
+ * Forward progress.  A digit pass is one launch of one block per tile whose
+ * tiles chain their digit counts through a decoupled look-back: a tile waits
+ * (a bounded spin) until the tiles before it have published theirs.  This
+ * assumes what the hardware dispatcher does when the launch has the device
+ * to itself: on each XCD the launch's blocks start in increasing tile order,
+ * so the smallest unfinished tile is always running or next to start, and a
+ * wait always ends.  Kernels the caller runs at the same time on other
+ * streams that hold every slot of one XCD for long can stall the tiles
+ * dealt to that XCD; the tiles waiting on them give up after FS_SPIN_LIMIT
+ * polls (2^24, seconds), and the sort then ends with FS_ERR_GPU_EXECUTION
+ * ("look-back wait exceeded its spin bound") at the next synchronizing call,
+ * its output unspecified.  Sorts of one sorter, and anything ordered with
+ * them on one stream, never wait on each other. */
 fs_status fs_sorter_with_context(int device, void *hip_stream, fs_sorter **out);
 
 /* Drop for GpuSorter: frees scratch, unloads the module, destroys an owned stream. */
@@ -138,6 +152,9 @@ fs_status fs_sort_pairs_buffer(fs_sorter *s, fs_key_type type, void *device_keys
  * waiting.  For FS_OP_ARGSORT `device_values` is the index output and
  * `device_keys` is read only; for FS_OP_SORT `device_values` is ignored.
  * Errors detected on the device are reported by the next fs_synchronize.
+ * The forward-progress assumption of fs_sorter_with_context holds here too:
+ * work on other streams that occupies a whole XCD for long while the sort
+ * runs can make it fail with FS_ERR_GPU_EXECUTION after the spin bound.
  *
  * HIP graph capture: fs_encode on a capturing stream records kernel launches
  * only (no memset, no allocation).  The graph then holds the addresses of the
@@ -225,7 +242,7 @@ typedef enum fs_test_option {
     FS_TEST_FUSED = 3,                  /* keys-only sorts begin with the fused first pass:
                                            0 = from FS_FUSED_MIN_KEYS keys on (the default),
                                            1 = never, 2 = at every size */
-    FS_TEST_TOP16 = 4,                  /* keys-only u32/i32 sorts take the top-16 launch sequence:
+    FS_TEST_TOP16 = 4,                  /* keys-only u32/i32/u64/i64 sorts take the top-16 launch sequence:
                                            0 = from FS_TOP16_MIN_KEYS keys on (the default),
                                            1 = never, 2 = at every size of at least 2 keys and
                                            on the top-16 path even where its region sample
@@ -242,16 +259,18 @@ fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t v
  * (measured for u32 and u64 keys). */
 #define FS_FUSED_MIN_KEYS 33554432u
 
-/* Keys-only u32 and i32 sorts from this many keys on, up to 2^16 times the
- * keys a local-sort block holds less five standard deviations (279,707,648
- * keys with the gfx950 build's 4,608-key blocks), take the top-16 path: the fused first pass on the second-highest byte, one stable
- * pass on the highest byte, then a local sort of every segment of keys that
- * share their top bits, in LDS - three reads and writes of the keys instead of
- * four.  f32 keys keep the LSD passes (their exponent bytes make segments
- * too large for one block), and so does an input whose region sample shows a
- * segment of more than 16 blocks' keys (constant or skewed top bytes): the
- * same launches then run the fused pass on the lowest byte and the stable
- * passes on the others. */
+/* Keys-only u32, i32, u64 and i64 sorts from this many keys on, up to 2^16
+ * times the keys a local-sort block holds less five standard deviations
+ * (gfx950 build: 280,035,328 32-bit keys with 4,608-key blocks, 135,266,304
+ * 64-bit keys with 2,304-key blocks), take the top-16 path: the fused first
+ * pass on the byte below the highest, one stable pass on the highest byte,
+ * then a local sort of every segment of keys that share their top bits, in
+ * LDS - three reads and writes of the keys instead of four (32-bit keys) or
+ * eight (64-bit keys).  Float keys keep the LSD passes (their exponent bytes
+ * make segments too large for one block), and so does an input whose region
+ * sample shows a segment of more than 16 blocks' keys (constant or skewed top
+ * bytes): the same launches then run the fused pass on the lowest byte and the
+ * stable passes on the others. */
 #define FS_TOP16_MIN_KEYS 33554432u
 
 /* How the last completed sort began: 0 = the histogram read (argsort, pairs,

@@ -265,10 +265,14 @@ void launch(const char* name, void (*entry)(void**), uint32_t grid, uint32_t blo
     if (getenv("EMU_TRACE")) fprintf(stderr, "hip_emu: launch %s grid=%u block=%u\n", name, grid, block);
     const int nx = xcds();
     int hold_queue = -1, hold_ms = 0;
+    bool hold_until_timeout = false;
     static std::atomic<bool> held{false};
     if (const char* h = getenv("EMU_HOLD_QUEUE"))
-        if (strncmp(name, "fs_onesweep", 11) == 0 && !held.exchange(true) && sscanf(h, "%d:%d", &hold_queue, &hold_ms) != 2)
-            hold_ms = 0;
+        if (strncmp(name, "fs_onesweep", 11) == 0 && !held.exchange(true)) {
+            char until[16] = {0};
+            if (sscanf(h, "%d:%15s", &hold_queue, until) == 2 && strcmp(until, "timeout") == 0) hold_until_timeout = true;
+            else if (sscanf(h, "%d:%d", &hold_queue, &hold_ms) != 2) hold_ms = 0;
+        }
     std::vector<std::atomic<uint32_t>> next(nx);           // per-queue position
     for (auto& c : next) c = 0;
     auto worker = [&](int queue) {
@@ -279,10 +283,22 @@ void launch(const char* name, void (*entry)(void**), uint32_t grid, uint32_t blo
             ss.ss_flags = 0;
             sigaltstack(&ss, nullptr);
         }
-        // EMU_HOLD_QUEUE=q:ms holds queue q of every digit-pass launch back for
-        // ms milliseconds, as if another stream's work occupied that XCD
-        // (the first digit-pass launch of the process only)
+        // EMU_HOLD_QUEUE=q:ms holds queue q of the first digit-pass launch of
+        // the process back for ms milliseconds, as if another stream's work
+        // occupied that XCD; q:timeout holds it until a look-back wait of the
+        // launch has ended at its spin bound (the status word says so), so
+        // that the outcome does not depend on timing
         if (hold_ms > 0 && queue == hold_queue) std::this_thread::sleep_for(std::chrono::milliseconds(hold_ms));
+        if (hold_until_timeout && queue == hold_queue) {
+            const volatile uint32_t* status = (const volatile uint32_t*)(uintptr_t)(*(FsArgs*)params[0]).status;
+            for (int ms = 0; !(*status & FS_DEVERR_LOOKBACK_TIMEOUT); ++ms) {
+                if (ms > 600000) {
+                    fprintf(stderr, "hip_emu: held queue %d: no look-back timeout within 600 s\n", queue);
+                    abort();
+                }
+                std::this_thread::sleep_for(std::chrono::milliseconds(1));
+            }
+        }
         for (;;) {
             const uint64_t b = (uint64_t)queue + (uint64_t)nx * next[queue].fetch_add(1);
             if (b >= grid) break;

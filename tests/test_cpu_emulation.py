@@ -187,11 +187,13 @@ def test_emulated_device_error_guards(emulator):
 
 
 def test_emulated_held_xcd_queue(emulator):
-    """One XCD queue of the first digit pass held back for a second (another
-    stream's work on that XCD): the look-back waits on its tiles end at the
-    spin bound with a clean GpuExecution, or the sort completes exactly; then
-    a sort is exact again."""
-    run_cases("faults", ["hold:u32:40000:uniform:1"], env={"EMU_CUS": "8", "EMU_HOLD_QUEUE": "3:1000"})
+    """One XCD queue of the first digit pass held back (another stream's work
+    on that XCD): held until a look-back wait on its tiles has reached the
+    spin bound (a build with a bound of 2,048 polls), the sort ends with a
+    clean GpuExecution; held for 50 ms, far within the product bound of 2^24
+    polls, it completes exactly; either way the next sort is exact."""
+    run_cases("faults", ["hold_timeout:u32:40000:uniform:1"], env={"EMU_CUS": "8", "EMU_HOLD_QUEUE": "3:timeout"})
+    run_cases("prod", ["hold_exact:u32:200000:uniform:2"], env={"EMU_CUS": "8", "EMU_HOLD_QUEUE": "3:50"})
 
 
 def test_emulated_no_alloc_entry_point(emulator):
