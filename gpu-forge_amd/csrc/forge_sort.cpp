@@ -42,11 +42,11 @@ const char* const kKernelNames[] = {
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
     "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
     "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_onesweep_loop_k32", "fs_local_k64",
-    "fs_local_deferred_k64",
+    "fs_local_deferred_k64", "fs_onesweep_loop_k64",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
-    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_LOCAL64, K_DEFER64, K_COUNT
+    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_LOCAL64, K_DEFER64, K_LOOP64, K_COUNT
 };
 
 }  // namespace
@@ -527,10 +527,13 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
             void* args2[] = {&a, &slot};
             // top-16 launch sequence: slot 0 is the top digit's pass, or on
             // the LSD passes the first of them; the other slots run only for
-            // those (32-bit keys: the loop kernel's small grid; 64-bit keys
-            // keep one block per tile: the loop kernel spills there)
-            const bool loop = top16 && sl > 0 && !key64(t);
-            if ((r = launch(s, loop ? K_LOOP32 : K_OS32 + var, loop ? small : num_tiles, s->block[var], args2, st,
+            // those, on the loop kernel's small grid (an idle launch costs a
+            // few blocks).  64-bit keys keep one block per tile for slot 1
+            // (u64 keys with up to 24 varying bits, which the sample sends to
+            // the LSD passes, run their last pass there at full speed).
+            const bool loop = top16 && sl >= (key64(t) ? 2u : 1u);
+            const int kl = key64(t) ? K_LOOP64 : K_LOOP32;
+            if ((r = launch(s, loop ? kl : K_OS32 + var, loop ? small : num_tiles, s->block[var], args2, st,
                             no_alloc)) != FS_OK)
                 return r;
         }

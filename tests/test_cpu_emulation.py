@@ -252,6 +252,7 @@ TOP16_SMALL = [
     "top16:u64:1025:low12:39", "top16:i64:9000:zipf:40", "top16over:u64:30000:grp2:41",
     "top16s16:u64:9000:uniform:42", "top16s12:i64:20000:uniform:43",
     "top16auto:u64:20000:uniform:44", "top16auto_lsd:u64:20000:top8:45", "top16auto_lsdover:i64:30000:top8grp0:46",
+    "top16auto_lsd:u64:9000:low12:47",
 ]
 
 
