@@ -19,6 +19,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -42,11 +43,11 @@ const char* const kKernelNames[] = {
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
     "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
     "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_onesweep_loop_k32", "fs_local_k64",
-    "fs_local_deferred_k64", "fs_onesweep_loop_k64",
+    "fs_local_deferred_k64", "fs_onesweep_loop_k64", "fs_local_deferred_k32",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
-    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_LOCAL64, K_DEFER64, K_LOOP64, K_COUNT
+    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_LOCAL64, K_DEFER64, K_LOOP64, K_DEFER32, K_COUNT
 };
 
 }  // namespace
@@ -61,6 +62,7 @@ struct fs_sorter {
     uint32_t block[4] = {};         // threads per block of each variant
     uint32_t local_keys[2] = {};    // keys a block of the local sort holds (fs_local_k32, fs_local_k64)
     uint32_t local_block[2] = {};   // their threads per block
+    uint32_t local_min_bits32 = 8;  // fewest segment bits whose 32-bit segments fs_local_k32 sorts itself
     int num_cus = 256;
 
     DevBuf s1k, s2k, s1v, s2v, lb0, lb1, iok, iov, tilemap;
@@ -489,7 +491,15 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.sub_keys = fused ? (uint32_t)sub_keys : 0u;
     a.s1_keys = fused ? (uint32_t)FS_FUSED_S1_KEYS(sub_keys) : 0u;
     a.segc = top16 ? sc.segc : 0u;
-    a.seg_bits = top16 ? (s->seg_bits ? s->seg_bits : seg_bits_for(n, local_keys_of(s, t))) : 0u;
+    a.seg_bits = !top16 ? 0u : s->seg_bits ? s->seg_bits : seg_bits_for(n, local_keys_of(s, t));
+    // 32-bit keys: at least the segment bits whose segments the local sort's
+    // first launch sorts itself, where that leaves a uniform input's segments
+    // a quarter of a block or more on average (from 2^25 keys on; smaller
+    // sorts, which take the top-16 path only when a test forces it, defer
+    // their segments to the second launch)
+    if (top16 && !s->seg_bits && !key64(t) && a.seg_bits < s->local_min_bits32 &&
+        (n >> s->local_min_bits32) >= local_keys_of(s, t) / 4u)
+        a.seg_bits = s->local_min_bits32;
     // a segment the region sample estimates above 16 blocks' keys sends the
     // sort to the LSD passes (unless a test forces the top-16 path)
     a.seg_limit = s->top16_mode == 2u ? 0xFFFFFFFFu : 16u * local_keys_of(s, t);
@@ -540,9 +550,11 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         if (top16 && (r = launch(s, key64(t) ? K_LOCAL64 : K_LOCAL32, 1u << a.seg_bits, s->local_block[key64(t) ? 1 : 0],
                                  args1, st, no_alloc)) != FS_OK)
             return r;
-        // 64-bit keys: the segments the local sort deferred (larger than a
-        // block, or many equal keys), on a small grid
-        if (top16 && key64(t) && (r = launch(s, K_DEFER64, small, s->local_block[1], args1, st, no_alloc)) != FS_OK)
+        // the segments the local sort deferred (larger than a block; 64-bit
+        // keys: many equal keys; 32-bit keys: fewer segment bits than it
+        // sorts in one stable pass), on a small grid
+        if (top16 && (r = launch(s, key64(t) ? K_DEFER64 : K_DEFER32, small, s->local_block[key64(t) ? 1 : 0], args1,
+                                 st, no_alloc)) != FS_OK)
             return r;
         s->last_stream = st;
         s->pending = true;
@@ -677,15 +689,16 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
                 return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object has an invalid tile geometry");
         hipDeviceptr_t lp = nullptr;
         size_t lsz = 0;
-        uint32_t lg[4] = {0, 0, 0, 0};
-        if (hipModuleGetGlobal(&lp, &lsz, s->module, "fs_kernel_local_geometry") != hipSuccess || lsz != 16 ||
-            hipMemcpyDtoH(lg, lp, 16) != hipSuccess || lg[0] == 0 || lg[1] < FS_RADIX || lg[2] == 0 ||
-            lg[3] < FS_RADIX)
+        uint32_t lg[5] = {0, 0, 0, 0, 0};
+        if (hipModuleGetGlobal(&lp, &lsz, s->module, "fs_kernel_local_geometry") != hipSuccess || lsz != 20 ||
+            hipMemcpyDtoH(lg, lp, 20) != hipSuccess || lg[0] == 0 || lg[1] < FS_RADIX || lg[2] == 0 ||
+            lg[3] < FS_RADIX || lg[4] < 8 || lg[4] > 16)
             return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object lacks a valid fs_kernel_local_geometry");
         for (int i = 0; i < 2; ++i) {
             s->local_keys[i] = lg[2 * i];
             s->local_block[i] = lg[2 * i + 1];
         }
+        s->local_min_bits32 = lg[4];
     }
     const size_t tab = (size_t)FS_MAX_DIGITS * FS_RADIX * 4;
     if (hipMalloc(&s->hist, (size_t)FS_HIST_WORDS * 4) != hipSuccess || hipMalloc(&s->binbase, tab) != hipSuccess ||

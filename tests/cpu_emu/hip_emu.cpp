@@ -213,19 +213,55 @@ static void run_block(uint32_t bid, uint32_t grid, uint32_t nthreads, void (*ent
         f.ctx.uc_link = nullptr;
         makecontext(&f.ctx, fiber_main, 0);
     }
+    // EMU_SCHED=wave / wave_rev: waves one at a time (in increasing or
+    // decreasing order), each run - its wave operations resolved at once -
+    // until every lane waits at a block barrier, has finished or spins; a wave
+    // then gets ahead of the others as far as the barriers allow, which shows
+    // a missing barrier between the waves' LDS accesses as a wrong result.
+    // Default: every runnable thread once per round, wave operations resolved
+    // after the round.
+    static const int sched_mode = [] {
+        const char* e = getenv("EMU_SCHED");
+        return !e ? 0 : strcmp(e, "wave") == 0 ? 1 : strcmp(e, "wave_rev") == 0 ? 2 : 0;
+    }();
+    const int nwaves = (b.nthreads + 63) / 64;
     for (;;) {
         bool ran = false, awake = false;
-        for (int i = 0; i < b.nthreads; ++i) {
-            if (b.f[i].state != RUNNABLE) continue;
-            if (!b.f[i].sleeping) awake = true;
-            b.f[i].sleeping = false;
-            b.cur = i;
-            swapcontext(&b.sched, &b.f[i].ctx);
-            ran = true;
-        }
-        b.cur = -1;
         bool resolved = false;
-        for (int w = 0; w * 64 < b.nthreads; ++w) resolved |= resolve_wave(w);
+        if (sched_mode == 0) {
+            for (int i = 0; i < b.nthreads; ++i) {
+                if (b.f[i].state != RUNNABLE) continue;
+                if (!b.f[i].sleeping) awake = true;
+                b.f[i].sleeping = false;
+                b.cur = i;
+                swapcontext(&b.sched, &b.f[i].ctx);
+                ran = true;
+            }
+            b.cur = -1;
+            for (int w = 0; w < nwaves; ++w) resolved |= resolve_wave(w);
+        } else {
+            for (int k = 0; k < nwaves; ++k) {
+                const int w = sched_mode == 1 ? k : nwaves - 1 - k;
+                const int lo = w * 64, hi = std::min(b.nthreads, lo + 64);
+                for (;;) {                               // this wave until it blocks or only spins
+                    bool wran = false, wawake = false;
+                    for (int i = lo; i < hi; ++i) {
+                        if (b.f[i].state != RUNNABLE) continue;
+                        if (!b.f[i].sleeping) wawake = true;
+                        b.f[i].sleeping = false;
+                        b.cur = i;
+                        swapcontext(&b.sched, &b.f[i].ctx);
+                        wran = true;
+                    }
+                    b.cur = -1;
+                    const bool wres = resolve_wave(w);
+                    ran |= wran;
+                    awake |= wawake;
+                    resolved |= wres;
+                    if (!wres && (!wran || !wawake)) break;
+                }
+            }
+        }
         int live = 0, at_bar = 0, orv = 0;
         for (auto& f : b.f) {
             if (f.state == DONE) continue;
@@ -331,6 +367,7 @@ void fs_first_k64(FsArgs);
 void fs_local_k32(FsArgs);
 void fs_local_k64(FsArgs);
 void fs_local_deferred_k64(FsArgs);
+void fs_local_deferred_k32(FsArgs);
 void fs_rescatter_k32(FsArgs);
 void fs_rescatter_k64(FsArgs);
 void fs_onesweep_loop_k32(FsArgs, uint32_t);
@@ -342,7 +379,7 @@ void fs_scratch_address(uint64_t*);
 void fs_gather_elems(uint64_t, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint64_t);
 extern uint32_t fs_kernel_tile_keys[4];
 extern uint32_t fs_kernel_block_threads[4];
-extern uint32_t fs_kernel_local_geometry[4];
+extern uint32_t fs_kernel_local_geometry[5];
 }
 
 struct emu_function {
@@ -366,6 +403,7 @@ static emu_function g_funcs[] = {
     {"fs_local_k32", [](void** p) { fs_local_k32(A0); }},
     {"fs_local_k64", [](void** p) { fs_local_k64(A0); }},
     {"fs_local_deferred_k64", [](void** p) { fs_local_deferred_k64(A0); }},
+    {"fs_local_deferred_k32", [](void** p) { fs_local_deferred_k32(A0); }},
     {"fs_rescatter_k32", [](void** p) { fs_rescatter_k32(A0); }},
     {"fs_rescatter_k64", [](void** p) { fs_rescatter_k64(A0); }},
     {"fs_onesweep_loop_k32", [](void** p) { fs_onesweep_loop_k32(A0, D1); }},

@@ -265,3 +265,22 @@ def test_emulated_top16_path(emulator):
                        "top16auto_lsd:u32:200000:top8:4", "top16:u64:200000:uniform:5", "top16:i64:60000:few:6",
                        "top16over:u64:300000:grp2:7"], timeout=900)
     run_cases("groups", ["top16:u32:70000:uniform:1", "top16over:i32:30000:grp2:2"], env={"EMU_CUS": "8"})
+
+
+WAVE_SERIAL_CASES = [
+    # every kernel family with more than one LDS phase per block: LSD passes
+    # (stable, argsort, pairs), the fused first pass, the top-16 path's local
+    # sorts with one and two stable passes, the 64-bit group sort and its LDS
+    # LSD fallback (many equal keys), the region sample's skewed counting
+    "sort:u32:3000:uniform:1", "argsort:f32:2000:few:2", "pairs:u64:1500:uniform:3",
+    "fused:u32:4000:uniform:4", "top16:u32:3000:uniform:5", "top16s12:u32:4000:uniform:6",
+    "top16:u64:3000:uniform:7", "top16:u64:1500:few:8", "top16auto_lsd:u32:9000:zipf:9",
+]
+
+
+@pytest.mark.parametrize("order", ["wave", "wave_rev"])
+def test_emulated_wave_serial_schedule(emulator, order):
+    """The same kernels with one wave of a block at a time, run as far as the
+    block barriers let it get ahead (forward and reverse wave order): a
+    missing barrier between waves' LDS accesses becomes a wrong result."""
+    run_cases("small", WAVE_SERIAL_CASES, timeout=900, env={"EMU_SCHED": order, "EMU_TEST_FUSED": "0"})
