@@ -254,8 +254,11 @@ static fs_status launch(fs_sorter* s, int k, unsigned grid, unsigned block, void
 
 // After a device error the histogram and the schedule (with the upsweep's
 // ticket) are cleared, so the next sort starts from the state every sort
-// leaves behind.  The device is idle here (the caller has synchronised).
+// leaves behind.  The whole device is drained first: a sort enqueued on
+// another stream (fs_encode with a caller's stream, a graph replay) may still
+// be using these tables.
 static void reset_device_tables(fs_sorter* s) {
+    (void)hipDeviceSynchronize();
     (void)hipMemset(s->hist, 0, (size_t)FS_HIST_WORDS * 4);
     (void)hipMemset(s->plan, 0, FS_PLAN_WORDS * sizeof(uint32_t));
     (void)hipMemset(s->cursors, 0, FS_REGIONS * sizeof(uint32_t));
