@@ -511,6 +511,30 @@ def test_top16_size_limit(sorter):
         del out
 
 
+def test_top16_size_limit_64(sorter):
+    """The same for u64 keys: the largest input the top-16 path takes by size
+    (2,304-key blocks of the 64-bit local sort) and one key more (the fused
+    LSD passes): ascending, same multiset."""
+    import math
+    local = 256 * 9                                    # keys of a 64-bit local-sort block (gfx950 build)
+    limit = (local - 5 * math.isqrt(local)) << 16
+    g = np.random.Generator(np.random.PCG64(981))
+    for n, expect in ((limit, 3), (limit + 1, 1)):
+        keys = g.integers(0, 1 << 64, size=n, dtype=np.uint64, endpoint=False)
+        s_sum = int(np.bitwise_xor.reduce(keys)), int((keys & np.uint64(0xFFFFFFFF)).sum()), int((keys >> np.uint64(32)).sum())
+        buf = sorter.alloc_sort_buffer("u64", n)
+        buf.copy_from_slice(keys)
+        del keys
+        sorter.sort_u64_buffer(buf)
+        assert sorter.first_pass() == expect
+        out = buf.as_slice()
+        buf.free()
+        assert bool(np.all(out[1:] >= out[:-1])), "not ascending"
+        assert (int(np.bitwise_xor.reduce(out)), int((out & np.uint64(0xFFFFFFFF)).sum()),
+                int((out >> np.uint64(32)).sum())) == s_sum
+        del out
+
+
 def test_fused_first_pass_2_31_keys(sorter):
     """The largest fused sort (n = 2^31, regions of S1 just below 2^32 keys
     in all) and one key more (the histogram read): ascending, same multiset."""
