@@ -31,13 +31,32 @@ def emulator():
     return EMU
 
 
-def run_cases(flavor, cases, timeout=300, env=None):
-    r = subprocess.run([sys.executable, os.path.join(EMU, "run_emu.py"), flavor, *cases],
-                       capture_output=True, text=True, timeout=timeout,
-                       env=dict(os.environ, **(env or {})))
-    lines = [ln for ln in r.stdout.splitlines() if ln.startswith(("PASS", "FAIL"))]
-    assert r.returncode == 0 and len(lines) == len(cases) and all(ln.startswith("PASS") for ln in lines), \
-        f"exit {r.returncode}\n{r.stdout}\n{r.stderr[-4000:]}"
+def run_cases(flavor, cases, timeout=300, env=None, parallel=1):
+    """Run the cases in `parallel` child processes at once (round-robin
+    shares of the list), each with its share of the emulator's worker
+    threads; every case must pass."""
+    parallel = max(1, min(parallel, len(cases)))
+    workers = max(1, (os.cpu_count() or 8) // parallel)
+    procs = []
+    for j in range(parallel):
+        share = cases[j::parallel]
+        e = dict(os.environ, **(env or {}))
+        if parallel > 1:
+            e.setdefault("EMU_WORKERS", str(workers))
+        procs.append((share, subprocess.Popen([sys.executable, os.path.join(EMU, "run_emu.py"), flavor, *share],
+                                              stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, env=e)))
+    lines = []
+    for share, p in procs:
+        try:
+            out, err = p.communicate(timeout=timeout)
+        except subprocess.TimeoutExpired:
+            for _, q in procs:
+                q.kill()
+            raise
+        got = [ln for ln in out.splitlines() if ln.startswith(("PASS", "FAIL"))]
+        assert p.returncode == 0 and len(got) == len(share) and all(ln.startswith("PASS") for ln in got), \
+            f"exit {p.returncode}\n{out}\n{err[-4000:]}"
+        lines += got
     return lines
 
 
@@ -77,7 +96,7 @@ PROD_CASES = [
 
 
 def test_emulated_small_tiles(emulator):
-    run_cases("small", SMALL_CASES)
+    run_cases("small", SMALL_CASES, parallel=4)
 
 
 def test_emulated_production_tiles(emulator):
@@ -110,7 +129,7 @@ def test_emulated_fused_first_pass(emulator):
     tiles a tile of the next pass spans dozens of regions, with production
     tiles a region spans several tiles; look-back groups of two tiles follow
     it in the groups build."""
-    run_cases("small", FUSED_SMALL)
+    run_cases("small", FUSED_SMALL, parallel=4)
     run_cases("prod", ["fused:u32:100000:uniform:1", "fused:f32:17665:uniform:2", "fused:u32:40000:byte0:3",
                        "fusedover:u32:450000:grp0:4", "nofused:u32:40000:uniform:5", "fused:u64:30000:uniform:6",
                        "fused:i64:8449:uniform:7", "fused:u32:40000:skew0:8"])
@@ -220,9 +239,9 @@ def test_emulated_sanitizers(emulator):
     run_cases("san", ["sort:u32:5000:uniform:1", "sort:f32:3001:uniform:3", "argsort:i32:2000:few:7",
                       "pairs:f64:2500:uniform:12", "sort:u32:5000:byte0:31", "sort:u32:9000:zipf:28",
                       "gather:u32:3000:uniform:26", "fused:u32:9000:uniform:40", "fusedover:u32:30000:grp0:41",
-                      "fused:u32:5000:byte0:42"],
+                      "fused:u32:5000:byte0:42", "top16:u64:1500:few:47"],
               timeout=600, env={"LD_PRELOAD": libasan, "EMU_NO_SEGV_HANDLER": "1", "EMU_CUS": "4", "EMU_TEST_FUSED": "2",
-                                "ASAN_OPTIONS": "detect_leaks=0:detect_stack_use_after_return=0"})
+                                "ASAN_OPTIONS": "detect_leaks=0:detect_stack_use_after_return=0"}, parallel=3)
 
 
 TOP16_SMALL = [
@@ -261,7 +280,7 @@ def test_emulated_top16_path(emulator):
     """Keys-only u32/i32/u64/i64 sorts on the top-16 launch sequence (region sample,
     fused pass, its re-scatter launch, digit passes, local sort): small
     tiles and blocks; production tiles; look-back groups of two tiles."""
-    run_cases("small", TOP16_SMALL, timeout=900)
+    run_cases("small", TOP16_SMALL, timeout=900, parallel=4)
     run_cases("prod", ["top16:u32:300000:uniform:1", "top16:i32:100000:few:2", "top16over:u32:450000:grp2:3",
                        "top16auto_lsd:u32:200000:top8:4", "top16:u64:200000:uniform:5", "top16:i64:60000:few:6",
                        "top16over:u64:300000:grp2:7"], timeout=900)
@@ -284,4 +303,4 @@ def test_emulated_wave_serial_schedule(emulator, order):
     """The same kernels with one wave of a block at a time, run as far as the
     block barriers let it get ahead (forward and reverse wave order): a
     missing barrier between waves' LDS accesses becomes a wrong result."""
-    run_cases("small", WAVE_SERIAL_CASES, timeout=900, env={"EMU_SCHED": order, "EMU_TEST_FUSED": "0"})
+    run_cases("small", WAVE_SERIAL_CASES, timeout=900, env={"EMU_SCHED": order, "EMU_TEST_FUSED": "0"}, parallel=3)
