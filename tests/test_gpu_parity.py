@@ -924,6 +924,52 @@ def test_graph_capture_replays(hip_stream, op):
         s.close()
 
 
+@pytest.mark.parametrize("kind", ["u32", "u64"])
+def test_graph_capture_replays_top16(hip_stream, kind):
+    """The top-16 launch sequence captured once and replayed on new data: the
+    region sample inside the graph picks, per replay, the top-16 path
+    (uniform keys; a region overflow re-scattered; many equal keys, whose
+    64-bit segments go to the deferred launch) or the LSD passes in the same
+    launches (two top-byte values), or nothing after the fused pass (equal
+    keys); eager sorts run between the replays; every replay is exact."""
+    import ctypes
+    from forge_sort import TEST_TOP16, TOP16_SAMPLED, OP_SORT, GpuSorter
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    st = ctypes.c_void_p(hip_stream)
+    s = GpuSorter.with_context(0, hip_stream)
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    s.set_test_option(TEST_TOP16, TOP16_SAMPLED)       # the sample chooses at this size
+    try:
+        n, n_other = 1_500_007, 200_001
+        tile = s.tile_config()["k64" if kind == "u64" else "k32"]
+        kb = s.alloc_sort_buffer(kind, n)
+        kb.copy_from_slice(make_keys(kind, n, "uniform", seed=930))
+        s.encode(OP_SORT, kind, kb.device_ptr(), None, n, stream=hip_stream)
+        s.reserve(OP_SORT, kind, n_other)
+        s.synchronize()                                 # scratch grown: the captured sort allocates nothing
+        assert hip.hipStreamBeginCapture(st, 0) == 0
+        s.encode(OP_SORT, kind, kb.device_ptr(), None, n, stream=hip_stream)
+        assert hip.hipStreamEndCapture(st, ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
+        for r, dist in enumerate(["uniform", "grp2", "top8", "dup", "same", "uniform"]):
+            keys = make_keys(kind, n, dist, seed=931 + r, tile=tile)
+            kb.copy_from_slice(keys)
+            assert hip.hipGraphLaunch(exe, st) == 0
+            assert hip.hipStreamSynchronize(st) == 0
+            assert np.array_equal(kb.as_slice(), oracle.sort(kind, keys)), f"replay {r} ({dist})"
+            other = make_keys(kind, n_other, "uniform", seed=960 + r)   # eager work between replays
+            got = other.copy()
+            getattr(s, f"sort_{kind}")(got)
+            assert np.array_equal(got, oracle.sort(kind, other))
+        kb.free()
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        s.close()
+
+
 def test_with_context_caller_stream(hip_stream):
     """GpuSorter::with_context on the caller's stream (lib.rs:606-686): every op
     and the async encode run there; results match the oracle."""
