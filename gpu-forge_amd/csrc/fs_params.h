@@ -134,8 +134,8 @@
 #define FS_PASS_REGIONED 4u  // the source is the fused first pass's region layout (see below)
 #define FS_PASS_SKEWED 8u    // a bin of the digit holds more than 1/FS_SKEW_SHARE of the keys: the
                              // pass's tile histogram uses replicated counters
-#define FS_PASS_SEGCOUNT 16u // the pass (digit 3 of the top-16 path, reading keys in digit-2 order)
-                             // adds the keys of every top-16-bit segment to FsArgs.segc
+#define FS_PASS_SEGCOUNT 16u // the pass (the top digit on the top-16 path, reading keys in the order of
+                             // the digit below) adds the keys of every top-16-bit segment to FsArgs.segc
 #ifndef FS_SKEW_SHARE
 #define FS_SKEW_SHARE 64u
 #endif
@@ -272,7 +272,7 @@
 #ifndef FS_L32_ITEMS
 #define FS_L32_ITEMS 18
 #endif
-// 64-bit keys: 256 x 9 keys per block (an 18 KiB stage: five blocks per CU)
+// 64-bit keys: 256 x 9 keys per block (an 18 KiB stage, 26 KiB of LDS: six blocks per CU)
 #ifndef FS_L64_BLOCK
 #define FS_L64_BLOCK 256
 #endif
