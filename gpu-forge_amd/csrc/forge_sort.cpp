@@ -42,12 +42,12 @@ const char* const kKernelNames[] = {
     "fs_upsweep_k32", "fs_upsweep_k64", "fs_onesweep_k32", "fs_onesweep_k32_v",
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
     "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
-    "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_onesweep_loop_k32", "fs_local_k64",
+    "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_local_k64",
     "fs_local_deferred_k64", "fs_onesweep_loop_k64", "fs_local_deferred_k32",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
-    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOOP32, K_LOCAL64, K_DEFER64, K_LOOP64, K_DEFER32, K_COUNT
+    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOCAL64, K_DEFER64, K_LOOP64, K_DEFER32, K_COUNT
 };
 
 }  // namespace
@@ -540,13 +540,14 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
             void* args2[] = {&a, &slot};
             // top-16 launch sequence: slot 0 is the top digit's pass, or on
             // the LSD passes the first of them; the other slots run only for
-            // those, on the loop kernel's small grid (an idle launch costs a
-            // few blocks).  64-bit keys keep one block per tile for slot 1
-            // (u64 keys with up to 24 varying bits, which the sample sends to
-            // the LSD passes, run their last pass there at full speed).
-            const bool loop = top16 && sl >= (key64(t) ? 2u : 1u);
-            const int kl = key64(t) ? K_LOOP64 : K_LOOP32;
-            if ((r = launch(s, loop ? kl : K_OS32 + var, loop ? small : num_tiles, s->block[var], args2, st,
+            // those.  They launch one block per tile (an idle launch: ~14 µs)
+            // so that inputs the sample sends to the LSD passes (narrow or
+            // skewed keys) run every pass at full speed; only 64-bit slots
+            // from FS_LOOP_SLOT64 on (keys with more than 40 varying bits
+            // whose top 16 bits the sample refused) take the loop kernel's
+            // small grid (idle: ~5 µs; working: one block per CU, slower).
+            const bool loop = top16 && key64(t) && sl >= FS_LOOP_SLOT64;
+            if ((r = launch(s, loop ? K_LOOP64 : K_OS32 + var, loop ? small : num_tiles, s->block[var], args2, st,
                             no_alloc)) != FS_OK)
                 return r;
         }

@@ -288,6 +288,13 @@
 #ifndef FS_L64_GLIM
 #define FS_L64_GLIM 32u
 #endif
+// 64-bit keys on the top-16 launch sequence: the digit-pass slots from this
+// one on (their 5th LSD pass and later, after the fused pass) are launched
+// on the persistent loop kernel's small grid; the earlier slots, and every
+// slot of 32-bit keys, launch one block per tile
+#ifndef FS_LOOP_SLOT64
+#define FS_LOOP_SLOT64 4u
+#endif
 
 // Error bits additionally reported through the status word.
 #define FS_DEVERR_BAD_TILE 2u        // a digit pass block mapped to a tile >= num_tiles

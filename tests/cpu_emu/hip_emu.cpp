@@ -370,7 +370,6 @@ void fs_local_deferred_k64(FsArgs);
 void fs_local_deferred_k32(FsArgs);
 void fs_rescatter_k32(FsArgs);
 void fs_rescatter_k64(FsArgs);
-void fs_onesweep_loop_k32(FsArgs, uint32_t);
 void fs_onesweep_loop_k64(FsArgs, uint32_t);
 void fs_region_sample_k32(FsArgs);
 void fs_region_sample_k64(FsArgs);
@@ -406,7 +405,6 @@ static emu_function g_funcs[] = {
     {"fs_local_deferred_k32", [](void** p) { fs_local_deferred_k32(A0); }},
     {"fs_rescatter_k32", [](void** p) { fs_rescatter_k32(A0); }},
     {"fs_rescatter_k64", [](void** p) { fs_rescatter_k64(A0); }},
-    {"fs_onesweep_loop_k32", [](void** p) { fs_onesweep_loop_k32(A0, D1); }},
     {"fs_onesweep_loop_k64", [](void** p) { fs_onesweep_loop_k64(A0, D1); }},
     {"fs_region_sample_k32", [](void** p) { fs_region_sample_k32(A0); }},
     {"fs_region_sample_k64", [](void** p) { fs_region_sample_k64(A0); }},

@@ -600,6 +600,26 @@ def test_config4_64bit(sorter, kind):
         check_buffer(sorter, "u64", datagen.low20_u64(n, high=0xABCDEF01234, seed=111))
 
 
+@pytest.mark.parametrize("kind,n,dist", [
+    ("u32", 1 << 28, "below 2^24"), ("i32", 1 << 28, "[-2^23, 2^23)"),
+    ("u64", 1 << 27, "below 2^40"), ("u64", 1 << 27, "below 2^48")])
+def test_top16_refused_full_size(sorter, kind, n, dist):
+    """Narrow keys at the top-16 path's sizes: their top 16 bits take few
+    values, the region sample refuses the path, and the LSD passes run in the
+    same launch sequence's digit-pass slots (one block per tile; 64-bit keys
+    from the fifth slot on, the persistent loop kernel: below 2^48 takes
+    slot 4).  Exact against the oracle."""
+    from forge_sort import FIRST_FUSED, FIRST_FUSED_OVERFLOW
+    g = np.random.Generator(np.random.PCG64(140 + n % 97 + len(dist)))
+    if kind == "i32":
+        keys = g.integers(-(1 << 23), 1 << 23, size=n, dtype=np.int32)
+    else:
+        top = {"below 2^24": 1 << 24, "below 2^40": 1 << 40, "below 2^48": 1 << 48}[dist]
+        keys = g.integers(0, top, size=n, dtype=np.uint32 if kind == "u32" else np.uint64)
+    check_buffer(sorter, kind, keys)
+    assert sorter.first_pass() in (FIRST_FUSED, FIRST_FUSED_OVERFLOW)
+
+
 @pytest.fixture
 def force_wide_lookback(sorter):
     """Select the 64-bit look-back tile entries (normally used from n = 2^30
