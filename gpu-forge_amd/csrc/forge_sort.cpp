@@ -321,8 +321,18 @@ static bool fused_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
 // Keys a block of the local sort holds for keys of this type.
 static uint32_t local_keys_of(const fs_sorter* s, fs_key_type t) { return s->local_keys[key64(t) ? 1 : 0]; }
 
-// Keys-only integer sorts (u32, i32, u64, i64) from FS_TOP16_MIN_KEYS keys
-// take the top-16 path (fused pass on the digit below the top byte, stable
+// The most keys a segment of a uniform input may hold on average for nearly
+// every segment to fit one block of the local sort: a block's keys less five
+// standard deviations (their square root).
+static uint64_t local_mean_max(const fs_sorter* s, fs_key_type t) {
+    const uint64_t lk = local_keys_of(s, t);
+    uint64_t root = 0;
+    while ((root + 1) * (root + 1) <= lk) ++root;
+    return lk > 5 * root ? lk - 5 * root : 0;
+}
+
+// Keys-only integer sorts (u32, i32 from FS_TOP16_MIN_KEYS32 keys, u64, i64
+// from FS_TOP16_MIN_KEYS64 keys) take the top-16 path (fused pass on the digit below the top byte, stable
 // pass on the top digit, local sort of each segment); it needs the fused
 // pass's regions, hence the fused range.  Float keys keep the LSD passes:
 // their top 16 bits (sign, exponent, a few mantissa bits) are concentrated
@@ -334,25 +344,21 @@ static bool top16_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
     if (FS_FUSED_S1_KEYS(fused_sub_keys(n, s->tile[variant_of(op, t)])) >= (1ull << 32)) return false;
     if (s->top16_mode >= 2u) return true;
     // By size: the 2^16 segments of a uniform input must fit a block with a
-    // margin of five standard deviations (local_keys - 5 sqrt(local_keys)
-    // keys each on average), so that hardly any takes the big-segment path.
-    const uint64_t lk = local_keys_of(s, t);
-    uint64_t root = 0;
-    while ((root + 1) * (root + 1) <= lk) ++root;
-    const uint64_t mean_max = lk > 5 * root ? lk - 5 * root : 0;
-    return n >= FS_TOP16_MIN_KEYS && n <= (mean_max << 16);
+    // margin of five standard deviations, so that hardly any takes the
+    // big-segment path.
+    return n >= (key64(t) ? FS_TOP16_MIN_KEYS64 : FS_TOP16_MIN_KEYS32) && n <= (local_mean_max(s, t) << 16);
 }
 
-// Bits that name a segment of the local sort: a uniform input's segment then
-// holds between a half and all of 2^floor(log2(block keys)) keys on average,
-// so that nearly every segment fits one block; at least the top byte, at
-// most the top 16 bits the two digit passes order.
-static uint32_t seg_bits_for(uint64_t n, uint32_t local_keys) {
-    uint32_t lg_n = 0, lg_c = 0;
-    while ((2ull << lg_n) <= n) ++lg_n;
-    while ((2ull << lg_c) <= local_keys) ++lg_c;
-    const int b = (int)lg_n - (int)lg_c;
-    return b < 8 ? 8u : b > 16 ? 16u : (uint32_t)b;
+// Bits that name a segment of the local sort: the fewest whose segments of
+// a uniform input hold at most mean_max keys on average (local_mean_max), so
+// that nearly every segment fits one block, but at least the top byte and at
+// most the top 16 bits the two digit passes order.  (Between a half and all
+// of mean_max keys each: fewer segment bits leave fewer bits to the local
+// sort.)
+static uint32_t seg_bits_for(uint64_t n, uint64_t mean_max) {
+    uint32_t b = 8;
+    while (b < 16 && n > (mean_max << b)) ++b;
+    return b;
 }
 
 // Grows the scratch a sort of n keys needs (grow-only, like ensure_buffers*,
@@ -494,7 +500,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.sub_keys = fused ? (uint32_t)sub_keys : 0u;
     a.s1_keys = fused ? (uint32_t)FS_FUSED_S1_KEYS(sub_keys) : 0u;
     a.segc = top16 ? sc.segc : 0u;
-    a.seg_bits = !top16 ? 0u : s->seg_bits ? s->seg_bits : seg_bits_for(n, local_keys_of(s, t));
+    a.seg_bits = !top16 ? 0u : s->seg_bits ? s->seg_bits : seg_bits_for(n, local_mean_max(s, t));
     // 32-bit keys: at least the segment bits whose segments the local sort's
     // first launch sorts itself, where that leaves a uniform input's segments
     // a quarter of a block or more on average (from 2^25 keys on; smaller

@@ -244,7 +244,7 @@
 #define FS_PLAN_RESCATTER (FS_PLAN_NPASSES + 6)
 #define FS_PLAN_WORDS (FS_PLAN_NPASSES + 8)
 
-// Top-16 path of keys-only integer sorts (from FS_TOP16_MIN_KEYS keys): the
+// Top-16 path of keys-only integer sorts (from FS_TOP16_MIN_KEYS32/64 keys): the
 // fused first pass scatters by the digit below the top byte (digit 2 of
 // 32-bit keys, 6 of 64-bit keys; the region sample's choice,
 // FS_RTABLE_SDIGIT) into its regions, a stable pass on the top digit reads

@@ -40,7 +40,8 @@ TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT, TEST_FUSED, T
 FUSED_BY_SIZE, FUSED_NEVER, FUSED_ALWAYS = 0, 1, 2       # TEST_FUSED values
 TOP16_BY_SIZE, TOP16_NEVER, TOP16_ALWAYS, TOP16_SAMPLED = 0, 1, 2, 3   # TEST_TOP16 values
 FUSED_MIN_KEYS = 1 << 25                                 # FS_FUSED_MIN_KEYS
-TOP16_MIN_KEYS = 1 << 25                                 # FS_TOP16_MIN_KEYS
+TOP16_MIN_KEYS32 = 44_040_192                            # FS_TOP16_MIN_KEYS32
+TOP16_MIN_KEYS64 = 1 << 21                               # FS_TOP16_MIN_KEYS64
 # fs_sorter_first_pass: how the last sort began
 FIRST_HISTOGRAM, FIRST_FUSED, FIRST_FUSED_OVERFLOW, FIRST_TOP16, FIRST_TOP16_RESCATTER = 0, 1, 2, 3, 4
 FAULT_NONE, FAULT_BAD_DIGITS, FAULT_BAD_BUFFER, FAULT_EXTRA_BLOCK, FAULT_STALL_TILE, FAULT_SMALL_S1 = 0, 1, 2, 3, 4, 5

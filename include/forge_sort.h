@@ -243,7 +243,7 @@ typedef enum fs_test_option {
                                            0 = from FS_FUSED_MIN_KEYS keys on (the default),
                                            1 = never, 2 = at every size */
     FS_TEST_TOP16 = 4,                  /* keys-only u32/i32/u64/i64 sorts take the top-16 launch sequence:
-                                           0 = from FS_TOP16_MIN_KEYS keys on (the default),
+                                           0 = from FS_TOP16_MIN_KEYS32/64 keys on (the default),
                                            1 = never, 2 = at every size of at least 2 keys and
                                            on the top-16 path even where its region sample
                                            estimates oversized segments, 3 = at every size,
@@ -259,19 +259,25 @@ fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t v
  * (measured for u32 and u64 keys). */
 #define FS_FUSED_MIN_KEYS 33554432u
 
-/* Keys-only u32, i32, u64 and i64 sorts from this many keys on, up to 2^16
- * times the keys a local-sort block holds less five standard deviations
- * (gfx950 build: 280,035,328 32-bit keys with 4,608-key blocks, 135,266,304
- * 64-bit keys with 2,304-key blocks), take the top-16 path: the fused first
- * pass on the byte below the highest, one stable pass on the highest byte,
- * then a local sort of every segment of keys that share their top bits, in
- * LDS - three reads and writes of the keys instead of four (32-bit keys) or
- * eight (64-bit keys).  Float keys keep the LSD passes (their exponent bytes
- * make segments too large for one block), and so does an input whose region
- * sample shows a segment of more than 16 blocks' keys (constant or skewed top
- * bytes): the same launches then run the fused pass on the lowest byte and the
- * stable passes on the others. */
-#define FS_TOP16_MIN_KEYS 33554432u
+/* Keys-only u32 and i32 sorts from FS_TOP16_MIN_KEYS32 keys on, u64 and i64
+ * sorts from FS_TOP16_MIN_KEYS64 keys on, up to 2^16 times the keys a
+ * local-sort block holds less five standard deviations (gfx950 build:
+ * 280,035,328 32-bit keys with 4,608-key blocks, 135,266,304 64-bit keys with
+ * 2,304-key blocks), take the top-16 path: the fused first pass on the byte
+ * below the highest, one stable pass on the highest byte, then a local sort of
+ * every segment of keys that share their top bits, in LDS - three reads and
+ * writes of the keys instead of four (32-bit keys) or eight (64-bit keys).
+ * Float keys keep the LSD passes (their exponent bytes make segments too large
+ * for one block), and so does an input whose region sample shows a segment of
+ * more than 16 blocks' keys (constant or skewed top bytes): the same launches
+ * then run the fused pass on the lowest byte and the stable passes on the
+ * others.  The thresholds are where the path measured faster than the LSD
+ * passes on one MI355X for uniform keys (32-bit keys: between 41.9M and 46.1M
+ * keys; 64-bit keys: between 65,536 and 131,072, taken at 2^21, where the
+ * launches of the sequence that a refused input leaves idle cost less than the
+ * path gains). */
+#define FS_TOP16_MIN_KEYS32 44040192u
+#define FS_TOP16_MIN_KEYS64 2097152u
 
 /* How the last completed sort began: 0 = the histogram read (argsort, pairs,
  * and keys-only sorts outside the fused range), 1 = the fused first pass of a

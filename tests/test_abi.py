@@ -83,4 +83,6 @@ def test_python_constants_match_the_header():
     h = open(os.path.join(ROOT, "include", "forge_sort.h")).read()
     val = lambda name: int(re.search(r"#define %s (\d+)u" % name, h).group(1))
     assert forge_sort.FUSED_MIN_KEYS == val("FS_FUSED_MIN_KEYS")
+    assert forge_sort.TOP16_MIN_KEYS32 == val("FS_TOP16_MIN_KEYS32")
+    assert forge_sort.TOP16_MIN_KEYS64 == val("FS_TOP16_MIN_KEYS64")
     assert forge_sort.NO_ALLOC_MAX_KEYS == val("FS_NO_ALLOC_MAX_KEYS")

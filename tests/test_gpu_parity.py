@@ -330,10 +330,12 @@ def test_fused_first_pass(sorter, kind, n, dist, expect):
     counts the upper digits and scatters by the lowest into regions), here
     forced at every size: exact against the oracle on both of its schedules,
     through the slice and buffer APIs; the histogram read gives the same keys."""
-    from forge_sort import FIRST_HISTOGRAM, FUSED_ALWAYS, FUSED_BY_SIZE, FUSED_NEVER, TEST_FUSED
+    from forge_sort import (FIRST_HISTOGRAM, FUSED_ALWAYS, FUSED_BY_SIZE, FUSED_NEVER, TEST_FUSED, TEST_TOP16,
+                            TOP16_BY_SIZE, TOP16_NEVER)
     keys = make_keys(kind, n, dist, seed=900 + n % 97,
                      tile=sorter.tile_config()[TILE_VARIANT[("sort", BITS[kind] == np.uint64)]])
     sorter.set_test_option(TEST_FUSED, FUSED_ALWAYS)
+    sorter.set_test_option(TEST_TOP16, TOP16_NEVER)      # (64-bit keys take it by size from 2^21 keys)
     try:
         check_sort(sorter, kind, keys)
         assert sorter.first_pass() == expect
@@ -352,14 +354,20 @@ def test_fused_first_pass(sorter, kind, n, dist, expect):
         hp, hm = sorter.last_pass_info()
         assert hm == (mask & ~1 if expect == 1 and dist == "byte1" else mask) and hp == bin(hm).count("1")
     finally:
+        sorter.set_test_option(TEST_TOP16, TOP16_BY_SIZE)
         sorter.set_test_option(TEST_FUSED, FUSED_BY_SIZE)
 
 
-@pytest.mark.parametrize("kind,n,expect", [("u32", 1 << 25, 3), ("f32", 1 << 25, 1), ("u32", (1 << 25) - 1, 0),
-                                            ("u32", 1 << 20, 0)])
+@pytest.mark.parametrize("kind,n,expect", [("u32", 1 << 25, 1), ("f32", 1 << 25, 1), ("u32", (1 << 25) - 1, 0),
+                                            ("u32", 1 << 20, 0), ("u32", 44_040_192 - 1, 1), ("u32", 44_040_192, 3),
+                                            ("u64", (1 << 21) - 1, 0), ("i64", 1 << 21, 3), ("f64", 1 << 21, 0)])
 def test_fused_first_pass_by_size(sorter, kind, n, expect):
-    """By default the fused first pass starts at FS_FUSED_MIN_KEYS keys,
-    where u32/i32 keys take the top-16 path (FS_TOP16_MIN_KEYS)."""
+    """By default the fused first pass starts at FS_FUSED_MIN_KEYS keys, and
+    keys-only integer sorts take the top-16 path from FS_TOP16_MIN_KEYS32
+    (u32/i32) or FS_TOP16_MIN_KEYS64 (u64/i64) keys, 64-bit keys below the
+    fused range too; float keys never."""
+    from forge_sort import TOP16_MIN_KEYS32, TOP16_MIN_KEYS64
+    assert (TOP16_MIN_KEYS32, TOP16_MIN_KEYS64) == (44_040_192, 1 << 21)
     keys = make_keys(kind, n, "uniform", seed=950)
     check_buffer(sorter, kind, keys)
     assert sorter.first_pass() == expect
@@ -444,12 +452,12 @@ def test_top16_path_64(sorter, kind, n, dist, expect):
 @pytest.mark.parametrize("dist,expect", [("uniform", (3,)), ("lowbits", (1,)), ("top8", (1,)), ("zipf", (1, 2)),
                                          ("same", (2,))])
 def test_top16_sample_chooses(sorter, dist, expect):
-    """By size (2^25 + 7 u32 keys) the region sample chooses: the top-16
+    """By size (FS_TOP16_MIN_KEYS32 + 7 u32 keys) the region sample chooses: the top-16
     path for a uniform input; the LSD passes in the same launches when it
     sees oversized segments (keys below 2^12, two top-byte values, Zipf ranks
     below 2^20, whose lowest byte may overflow a region: re-scattered); no
     pass after the fused one when every digit is constant."""
-    keys = make_keys("u32", (1 << 25) + 7, dist, seed=975)
+    keys = make_keys("u32", 44_040_192 + 7, dist, seed=975)
     check_buffer(sorter, "u32", keys)
     assert sorter.first_pass() in expect
 

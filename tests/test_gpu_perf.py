@@ -94,8 +94,8 @@ def test_perf_slice(sorter, case, seed, floor):
 # (case, seed, floor in Mkeys/s): device-resident, floors about half the
 # rates measured on one MI355X
 DEVICE_CASES = [("sort_u32", 42, 35000.0), ("sort_i32", 43, 35000.0), ("sort_f32", 44, 30000.0),
-                ("argsort_u32", 45, 25000.0), ("sort_pairs_f32", 46, 20000.0), ("sort_u64", 47, 10000.0),
-                ("sort_i64", 48, 10000.0), ("sort_f64", 49, 10000.0)]
+                ("argsort_u32", 45, 25000.0), ("sort_pairs_f32", 46, 20000.0), ("sort_u64", 47, 25000.0),
+                ("sort_i64", 48, 25000.0), ("sort_f64", 49, 10000.0)]
 
 
 @pytest.mark.parametrize("case,seed,floor", DEVICE_CASES)
@@ -142,3 +142,44 @@ def test_perf_device(sorter, case, seed, floor):
         src.free()
     print(f"{case} device 16M: {mks:,.0f} Mkeys/s (floor {floor:,.0f})")
     assert mks >= floor, f"{case}: {mks:,.0f} Mkeys/s < {floor:,.0f}"
+
+
+# (key type, n, floor in Mkeys/s): keys-only sorts on the top-16 path at sizes
+# between powers of two, where the segment bits must still keep a uniform
+# input's segments within a block (floors about half the rates measured on
+# one MI355X: u32 100M 111,900, 200M 128,300; u64 50M 66,000, 100M 74,000)
+BETWEEN_CASES = [("u32", 100_000_000, 55000.0), ("u32", 200_000_000, 64000.0),
+                 ("u64", 50_000_000, 33000.0), ("u64", 100_000_000, 37000.0)]
+
+
+@pytest.mark.parametrize("kind,n,floor", BETWEEN_CASES)
+def test_perf_device_between_powers_of_two(sorter, kind, n, floor):
+    """Device-resident uniform keys at sizes that are not powers of two:
+    the median of 10 sorts (a device copy of the input before each, untimed)."""
+    dt = np.uint32 if kind == "u32" else np.uint64
+    keys = rng(50 + n % 89).integers(0, 1 << (8 * np.dtype(dt).itemsize), size=n, dtype=dt, endpoint=False)
+    src = sorter.alloc_sort_buffer(kind, n)
+    src.copy_from_slice(keys)
+    work = sorter.alloc_sort_buffer(kind, n)
+    try:
+        def copy_keys():
+            sorter.copy_device(work.device_ptr(), src.device_ptr(), keys.itemsize * n)
+            sorter.device_synchronize()
+        copy_keys()
+        sorter.sort_device(kind, work.device_ptr(), n)
+        times = []
+        for _ in range(REPS):
+            copy_keys()
+            t0 = time.perf_counter()
+            sorter.sort_device(kind, work.device_ptr(), n)
+            times.append(time.perf_counter() - t0)
+        mks = n / float(np.median(times)) / 1e6
+        work.set_len(n)
+        out = work.as_slice()
+        assert bool(np.all(out[1:] >= out[:-1])), "not ascending"
+        assert sorter.first_pass() == 3, "expected the top-16 path"
+    finally:
+        work.free()
+        src.free()
+    print(f"sort_{kind} device {n:,}: {mks:,.0f} Mkeys/s (floor {floor:,.0f})")
+    assert mks >= floor, f"sort_{kind} {n:,}: {mks:,.0f} Mkeys/s < {floor:,.0f}"
