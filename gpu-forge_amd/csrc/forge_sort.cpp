@@ -43,11 +43,13 @@ const char* const kKernelNames[] = {
     "fs_onesweep_k64", "fs_onesweep_k64_v", "fs_iota", "fs_onesweep_any_k32", "fs_onesweep_any_k64",
     "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
     "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_local_k64",
-    "fs_local_deferred_k64", "fs_onesweep_loop_k64", "fs_local_deferred_k32",
+    "fs_local_deferred_k64", "fs_onesweep_loop_k64", "fs_local_deferred_k32", "fs_local_k32_w",
+    "fs_local_deferred_k32_w", "fs_local_k64_w", "fs_local_deferred_k64_w",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
-    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOCAL64, K_DEFER64, K_LOOP64, K_DEFER32, K_COUNT
+    K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOCAL64, K_DEFER64, K_LOOP64, K_DEFER32,
+    K_LOCAL32W, K_DEFER32W, K_LOCAL64W, K_DEFER64W, K_COUNT
 };
 
 }  // namespace
@@ -60,8 +62,10 @@ struct fs_sorter {
     hipFunction_t fn[K_COUNT] = {};
     uint32_t tile[4] = {};          // keys per tile of each digit-pass variant (FS_VAR_*)
     uint32_t block[4] = {};         // threads per block of each variant
-    uint32_t local_keys[2] = {};    // keys a block of the local sort holds (fs_local_k32, fs_local_k64)
-    uint32_t local_block[2] = {};   // their threads per block
+    // keys a block of the local sort holds and its threads per block, by
+    // [wide][64-bit keys] (fs_local_k32, fs_local_k64, fs_local_k32_w, fs_local_k64_w)
+    uint32_t local_keys[2][2] = {};
+    uint32_t local_block[2][2] = {};
     uint32_t local_min_bits32 = 8;  // fewest segment bits whose 32-bit segments fs_local_k32 sorts itself
     int num_cus = 256;
 
@@ -92,6 +96,7 @@ struct fs_sorter {
     uint32_t fused_mode = 0;             // FS_TEST_FUSED: 0 by size, 1 never, 2 always
     uint32_t top16_mode = 0;             // FS_TEST_TOP16: 0 by size, 1 never, 2 always (even skewed), 3 sampled
     uint32_t seg_bits = 0;               // FS_TEST_SEG_BITS: 0 by size, else the segment bits
+    uint32_t local_wide_mode = 0;        // FS_TEST_LOCAL_WIDE: 0 by size, 1 wide local-sort blocks
     // the last sort's schedule (the sorter's, or the static scratch's) and
     // whether it began with the fused first pass
     uint32_t* last_plan = nullptr;
@@ -318,14 +323,16 @@ static bool fused_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
     return s->fused_mode == 2u || n >= FS_FUSED_MIN_KEYS;
 }
 
-// Keys a block of the local sort holds for keys of this type.
-static uint32_t local_keys_of(const fs_sorter* s, fs_key_type t) { return s->local_keys[key64(t) ? 1 : 0]; }
+// Keys a block of the local sort (wide: its wide blocks) holds for keys of this type.
+static uint32_t local_keys_of(const fs_sorter* s, fs_key_type t, bool wide) {
+    return s->local_keys[wide ? 1 : 0][key64(t) ? 1 : 0];
+}
 
 // The most keys a segment of a uniform input may hold on average for nearly
 // every segment to fit one block of the local sort: a block's keys less five
 // standard deviations (their square root).
-static uint64_t local_mean_max(const fs_sorter* s, fs_key_type t) {
-    const uint64_t lk = local_keys_of(s, t);
+static uint64_t local_mean_max(const fs_sorter* s, fs_key_type t, bool wide) {
+    const uint64_t lk = local_keys_of(s, t, wide);
     uint64_t root = 0;
     while ((root + 1) * (root + 1) <= lk) ++root;
     return lk > 5 * root ? lk - 5 * root : 0;
@@ -343,10 +350,16 @@ static bool top16_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
     if (n > (1ull << 31) || s->fused_mode == 1u) return false;
     if (FS_FUSED_S1_KEYS(fused_sub_keys(n, s->tile[variant_of(op, t)])) >= (1ull << 32)) return false;
     if (s->top16_mode >= 2u) return true;
-    // By size: the 2^16 segments of a uniform input must fit a block with a
-    // margin of five standard deviations, so that hardly any takes the
-    // big-segment path.
-    return n >= (key64(t) ? FS_TOP16_MIN_KEYS64 : FS_TOP16_MIN_KEYS32) && n <= (local_mean_max(s, t) << 16);
+    // By size: the 2^16 segments of a uniform input must fit a block (a wide
+    // one from the sizes local_wide names on) with a margin of five standard
+    // deviations, so that hardly any takes the big-segment path.
+    return n >= (key64(t) ? FS_TOP16_MIN_KEYS64 : FS_TOP16_MIN_KEYS32) && n <= (local_mean_max(s, t, true) << 16);
+}
+
+// The top-16 path's local sort runs on wide blocks (twice the keys) where
+// the 2^16 segments of a uniform input would outgrow the other blocks.
+static bool local_wide(const fs_sorter* s, fs_key_type t, uint64_t n) {
+    return s->local_wide_mode == 1u || n > (local_mean_max(s, t, false) << 16);
 }
 
 // Bits that name a segment of the local sort: the fewest whose segments of
@@ -500,18 +513,19 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     a.sub_keys = fused ? (uint32_t)sub_keys : 0u;
     a.s1_keys = fused ? (uint32_t)FS_FUSED_S1_KEYS(sub_keys) : 0u;
     a.segc = top16 ? sc.segc : 0u;
-    a.seg_bits = !top16 ? 0u : s->seg_bits ? s->seg_bits : seg_bits_for(n, local_mean_max(s, t));
+    const bool wide_local = top16 && local_wide(s, t, n);
+    a.seg_bits = !top16 ? 0u : s->seg_bits ? s->seg_bits : seg_bits_for(n, local_mean_max(s, t, wide_local));
     // 32-bit keys: at least the segment bits whose segments the local sort's
     // first launch sorts itself, where that leaves a uniform input's segments
     // a quarter of a block or more on average (from 2^25 keys on; smaller
     // sorts, which take the top-16 path only when a test forces it, defer
     // their segments to the second launch)
     if (top16 && !s->seg_bits && !key64(t) && a.seg_bits < s->local_min_bits32 &&
-        (n >> s->local_min_bits32) >= local_keys_of(s, t) / 4u)
+        (n >> s->local_min_bits32) >= local_keys_of(s, t, wide_local) / 4u)
         a.seg_bits = s->local_min_bits32;
     // a segment the region sample estimates above 16 blocks' keys sends the
     // sort to the LSD passes (unless a test forces the top-16 path)
-    a.seg_limit = s->top16_mode == 2u ? 0xFFFFFFFFu : 16u * local_keys_of(s, t);
+    a.seg_limit = s->top16_mode == 2u ? 0xFFFFFFFFu : 16u * local_keys_of(s, t, wide_local);
     a.status = (uint64_t)(uintptr_t)s->status;
     a.stats = s->stats_on ? (uint64_t)(uintptr_t)s->stats : 0u;
 #ifdef FS_FAULT_INJECTION
@@ -557,14 +571,15 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
                             no_alloc)) != FS_OK)
                 return r;
         }
-        if (top16 && (r = launch(s, key64(t) ? K_LOCAL64 : K_LOCAL32, 1u << a.seg_bits, s->local_block[key64(t) ? 1 : 0],
-                                 args1, st, no_alloc)) != FS_OK)
+        const uint32_t lthreads = s->local_block[wide_local ? 1 : 0][key64(t) ? 1 : 0];
+        const int klocal = wide_local ? (key64(t) ? K_LOCAL64W : K_LOCAL32W) : (key64(t) ? K_LOCAL64 : K_LOCAL32);
+        const int kdefer = wide_local ? (key64(t) ? K_DEFER64W : K_DEFER32W) : (key64(t) ? K_DEFER64 : K_DEFER32);
+        if (top16 && (r = launch(s, klocal, 1u << a.seg_bits, lthreads, args1, st, no_alloc)) != FS_OK)
             return r;
         // the segments the local sort deferred (larger than a block; 64-bit
         // keys: many equal keys; 32-bit keys: fewer segment bits than it
         // sorts in one stable pass), on a small grid
-        if (top16 && (r = launch(s, key64(t) ? K_DEFER64 : K_DEFER32, small, s->local_block[key64(t) ? 1 : 0], args1,
-                                 st, no_alloc)) != FS_OK)
+        if (top16 && (r = launch(s, kdefer, small, lthreads, args1, st, no_alloc)) != FS_OK)
             return r;
         s->last_stream = st;
         s->pending = true;
@@ -699,15 +714,18 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
                 return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object has an invalid tile geometry");
         hipDeviceptr_t lp = nullptr;
         size_t lsz = 0;
-        uint32_t lg[5] = {0, 0, 0, 0, 0};
-        if (hipModuleGetGlobal(&lp, &lsz, s->module, "fs_kernel_local_geometry") != hipSuccess || lsz != 20 ||
-            hipMemcpyDtoH(lg, lp, 20) != hipSuccess || lg[0] == 0 || lg[1] < FS_RADIX || lg[2] == 0 ||
-            lg[3] < FS_RADIX || lg[4] < 8 || lg[4] > 16)
+        uint32_t lg[9] = {};
+        if (hipModuleGetGlobal(&lp, &lsz, s->module, "fs_kernel_local_geometry") != hipSuccess ||
+            lsz != sizeof(lg) || hipMemcpyDtoH(lg, lp, sizeof(lg)) != hipSuccess || lg[4] < 8 || lg[4] > 16)
             return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object lacks a valid fs_kernel_local_geometry");
-        for (int i = 0; i < 2; ++i) {
-            s->local_keys[i] = lg[2 * i];
-            s->local_block[i] = lg[2 * i + 1];
-        }
+        for (int w = 0; w < 2; ++w)
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t keys = lg[w ? 5 + 2 * i : 2 * i], threads = lg[w ? 6 + 2 * i : 2 * i + 1];
+                if (keys == 0 || threads < FS_RADIX)
+                    return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object has an invalid local geometry");
+                s->local_keys[w][i] = keys;
+                s->local_block[w][i] = threads;
+            }
         s->local_min_bits32 = lg[4];
     }
     const size_t tab = (size_t)FS_MAX_DIGITS * FS_RADIX * 4;
@@ -918,6 +936,11 @@ fs_status fs_sorter_set_test_option(fs_sorter* s, fs_test_option opt, uint64_t v
         case FS_TEST_TOP16:
             if (value > 3) return set_err(s, FS_ERR_INVALID_ARGUMENT, "top-16 mode %llu > 3", (unsigned long long)value);
             s->top16_mode = (uint32_t)value;
+            return FS_OK;
+        case FS_TEST_LOCAL_WIDE:
+            if (value > 1) return set_err(s, FS_ERR_INVALID_ARGUMENT, "local-sort block choice %llu > 1",
+                                          (unsigned long long)value);
+            s->local_wide_mode = (uint32_t)value;
             return FS_OK;
         case FS_TEST_SEG_BITS:
             if (value != 0 && (value < 8 || value > 16))

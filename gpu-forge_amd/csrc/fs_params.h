@@ -288,6 +288,13 @@
 #ifndef FS_L64_GLIM
 #define FS_L64_GLIM 32u
 #endif
+// Wide local-sort blocks (the same keys per thread, FS_LW_BLOCK threads):
+// sorts too large for 2^16 segments of the blocks above to fit them (more
+// than 280M 32-bit or 135M 64-bit keys) take the top-16 path on these, up
+// to twice those sizes
+#ifndef FS_LW_BLOCK
+#define FS_LW_BLOCK 512
+#endif
 // 64-bit keys on the top-16 launch sequence: the digit-pass slots from this
 // one on (their 5th LSD pass and later, after the fused pass) are launched
 // on the persistent loop kernel's small grid; the earlier slots, and every

@@ -37,6 +37,7 @@ NO_ALLOC_MAX_KEYS = 1 << 20          # FS_NO_ALLOC_MAX_KEYS
 # fs_test_option and the FS_FAULT_* codes (include/forge_sort.h, csrc/fs_params.h)
 TEST_WIDE_LOOKBACK, TEST_UPSWEEP_BLOCKS_PER_CU, TEST_INJECT_FAULT, TEST_FUSED, TEST_TOP16, TEST_SEG_BITS = \
     0, 1, 2, 3, 4, 5
+TEST_LOCAL_WIDE = 6
 FUSED_BY_SIZE, FUSED_NEVER, FUSED_ALWAYS = 0, 1, 2       # TEST_FUSED values
 TOP16_BY_SIZE, TOP16_NEVER, TOP16_ALWAYS, TOP16_SAMPLED = 0, 1, 2, 3   # TEST_TOP16 values
 FUSED_MIN_KEYS = 1 << 25                                 # FS_FUSED_MIN_KEYS

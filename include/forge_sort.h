@@ -248,8 +248,11 @@ typedef enum fs_test_option {
                                            on the top-16 path even where its region sample
                                            estimates oversized segments, 3 = at every size,
                                            the sample choosing as by default */
-    FS_TEST_SEG_BITS = 5                /* top-16 path: 0 = segment bits by size (the default),
+    FS_TEST_SEG_BITS = 5,               /* top-16 path: 0 = segment bits by size (the default),
                                            8..16 = segments named by that many top bits */
+    FS_TEST_LOCAL_WIDE = 6              /* top-16 path: 0 = wide local-sort blocks by size (the
+                                           default: beyond the other blocks' size limit),
+                                           1 = wide blocks at every size */
 } fs_test_option;
 fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t value);
 
@@ -260,10 +263,11 @@ fs_status fs_sorter_set_test_option(fs_sorter *s, fs_test_option opt, uint64_t v
 #define FS_FUSED_MIN_KEYS 33554432u
 
 /* Keys-only u32 and i32 sorts from FS_TOP16_MIN_KEYS32 keys on, u64 and i64
- * sorts from FS_TOP16_MIN_KEYS64 keys on, up to 2^16 times the keys a
+ * sorts from FS_TOP16_MIN_KEYS64 keys on, up to 2^16 times the keys a wide
  * local-sort block holds less five standard deviations (gfx950 build:
- * 280,035,328 32-bit keys with 4,608-key blocks, 135,266,304 64-bit keys with
- * 2,304-key blocks), take the top-16 path: the fused first pass on the byte
+ * 572,522,496 32-bit keys with 9,216-key blocks, 280,035,328 64-bit keys with
+ * 4,608-key blocks; up to 280,035,328 and 135,266,304 keys the blocks of half
+ * that size sort the segments, at lower cost per key), take the top-16 path: the fused first pass on the byte
  * below the highest, one stable pass on the highest byte, then a local sort of
  * every segment of keys that share their top bits, in LDS - three reads and
  * writes of the keys instead of four (32-bit keys) or eight (64-bit keys).

@@ -368,6 +368,10 @@ void fs_local_k32(FsArgs);
 void fs_local_k64(FsArgs);
 void fs_local_deferred_k64(FsArgs);
 void fs_local_deferred_k32(FsArgs);
+void fs_local_k32_w(FsArgs);
+void fs_local_deferred_k32_w(FsArgs);
+void fs_local_k64_w(FsArgs);
+void fs_local_deferred_k64_w(FsArgs);
 void fs_rescatter_k32(FsArgs);
 void fs_rescatter_k64(FsArgs);
 void fs_onesweep_loop_k64(FsArgs, uint32_t);
@@ -378,7 +382,7 @@ void fs_scratch_address(uint64_t*);
 void fs_gather_elems(uint64_t, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint64_t);
 extern uint32_t fs_kernel_tile_keys[4];
 extern uint32_t fs_kernel_block_threads[4];
-extern uint32_t fs_kernel_local_geometry[5];
+extern uint32_t fs_kernel_local_geometry[9];
 }
 
 struct emu_function {
@@ -403,6 +407,10 @@ static emu_function g_funcs[] = {
     {"fs_local_k64", [](void** p) { fs_local_k64(A0); }},
     {"fs_local_deferred_k64", [](void** p) { fs_local_deferred_k64(A0); }},
     {"fs_local_deferred_k32", [](void** p) { fs_local_deferred_k32(A0); }},
+    {"fs_local_k32_w", [](void** p) { fs_local_k32_w(A0); }},
+    {"fs_local_deferred_k32_w", [](void** p) { fs_local_deferred_k32_w(A0); }},
+    {"fs_local_k64_w", [](void** p) { fs_local_k64_w(A0); }},
+    {"fs_local_deferred_k64_w", [](void** p) { fs_local_deferred_k64_w(A0); }},
     {"fs_rescatter_k32", [](void** p) { fs_rescatter_k32(A0); }},
     {"fs_rescatter_k64", [](void** p) { fs_rescatter_k64(A0); }},
     {"fs_onesweep_loop_k64", [](void** p) { fs_onesweep_loop_k64(A0, D1); }},

@@ -289,6 +289,10 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
     (fs_sorter_first_pass), with the fused first pass at every size, or
     ("nofused") never."""
     keys = keys_for(kind, n, dist, seed, tile=sorter.tile_config()["k64" if BITS[kind] == np.uint64 else "k32"])
+    # top16w...: the same case on the wide local-sort blocks
+    wide = op.startswith("top16w")
+    if wide:
+        op = "top16" + op[6:]
     top16 = op.startswith("top16")
     sorter.set_test_option(forge_sort.TEST_FUSED,
                            forge_sort.FUSED_NEVER if op == "nofused" else forge_sort.FUSED_ALWAYS)
@@ -296,6 +300,7 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
                            else forge_sort.TOP16_ALWAYS if top16 else forge_sort.TOP16_NEVER)
     # top16s<bits>: segments named by that many top bits
     sorter.set_test_option(forge_sort.TEST_SEG_BITS, int(op[6:]) if op.startswith("top16s") else 0)
+    sorter.set_test_option(forge_sort.TEST_LOCAL_WIDE, 1 if wide else 0)
     try:
         ok = sorted_ok(sorter, kind, keys)
         first = sorter.first_pass()
@@ -304,6 +309,7 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
         sorter.set_test_option(forge_sort.TEST_FUSED, FUSED_MODE)
         sorter.set_test_option(forge_sort.TEST_TOP16, TOP16_MODE)
         sorter.set_test_option(forge_sort.TEST_SEG_BITS, 0)
+        sorter.set_test_option(forge_sort.TEST_LOCAL_WIDE, 0)
     expect = FIRST_PASS["top16" if op.startswith("top16s") else op]
     if top16 and dist == "same" and not op.startswith("top16auto"):
         expect = forge_sort.FIRST_TOP16               # forced onto the top-16 path: one segment of every key
@@ -313,12 +319,13 @@ def check_first_pass(sorter, op, kind, n, dist, seed):
     if dist == "same" and passes != 0 and expect != forge_sort.FIRST_TOP16:
         print(f"  equal keys ran {passes} passes", flush=True)
         ok = False
-    print(f"{'PASS' if ok else 'FAIL'} {op} {kind} n={n} {dist} passes={passes} mask={mask:#x}", flush=True)
+    print(f"{'PASS' if ok else 'FAIL'} {op}{' (wide)' if wide else ''} {kind} n={n} {dist} passes={passes} "
+          f"mask={mask:#x}", flush=True)
     return ok
 
 
 def check(sorter, op, kind, n, dist, seed):
-    if op in FIRST_PASS or op.startswith("top16s"):
+    if op in FIRST_PASS or op.startswith(("top16s", "top16w")):
         return check_first_pass(sorter, op, kind, n, dist, seed)
     if op == "noalloc":
         ok = check_no_alloc(sorter, kind, n, dist, seed)

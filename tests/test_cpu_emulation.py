@@ -273,6 +273,12 @@ TOP16_SMALL = [
     "top16s12:i64:20000:uniform:43",
     "top16auto:u64:20000:uniform:44", "top16auto_lsd:u64:20000:top8:45", "top16auto_lsdover:i64:30000:top8grp0:46",
     "top16auto_lsd:u64:9000:low12:47",
+    # the wide local-sort blocks (FS_LW_BLOCK threads, which sorts beyond the
+    # other blocks' size limit take): both key widths, every local plan,
+    # equal keys (64-bit LSD fallback in LDS), a re-scattered region
+    "top16w:u32:5000:uniform:51", "top16w:u32:3000:few:52", "top16wover:i32:30000:grp2:53",
+    "top16ws12:u32:20000:uniform:54", "top16w:u64:3000:uniform:55", "top16w:i64:1500:few:56",
+    "top16w:u64:5000:top8:57", "top16wover:u64:30000:grp2:58",
 ]
 
 
@@ -283,7 +289,8 @@ def test_emulated_top16_path(emulator):
     run_cases("small", TOP16_SMALL, timeout=900, parallel=4)
     run_cases("prod", ["top16:u32:300000:uniform:1", "top16:i32:100000:few:2", "top16over:u32:450000:grp2:3",
                        "top16auto_lsd:u32:200000:top8:4", "top16:u64:200000:uniform:5", "top16:i64:60000:few:6",
-                       "top16over:u64:300000:grp2:7"], timeout=900)
+                       "top16over:u64:300000:grp2:7", "top16w:u32:300000:uniform:8", "top16w:u64:200000:few:9"],
+              timeout=900)
     run_cases("groups", ["top16:u32:70000:uniform:1", "top16over:i32:30000:grp2:2"], env={"EMU_CUS": "8"})
 
 
@@ -295,6 +302,7 @@ WAVE_SERIAL_CASES = [
     "sort:u32:3000:uniform:1", "argsort:f32:2000:few:2", "pairs:u64:1500:uniform:3",
     "fused:u32:4000:uniform:4", "top16:u32:3000:uniform:5", "top16s12:u32:4000:uniform:6",
     "top16:u64:3000:uniform:7", "top16:u64:1500:few:8", "top16auto_lsd:u32:9000:zipf:9",
+    "top16w:u32:3000:uniform:10", "top16w:u64:1500:few:11",
 ]
 
 

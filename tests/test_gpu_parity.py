@@ -495,14 +495,22 @@ def test_top16_segment_bits(sorter, bits, dist):
         sorter.set_test_option(TEST_TOP16, TOP16_BY_SIZE)
 
 
-def test_top16_size_limit(sorter):
-    """The largest input the top-16 path takes by size (its segments of a
-    uniform input within a block's keys, with a five-sigma margin) and one
-    key more (the fused LSD passes): ascending, same multiset."""
+def top16_limits(block_keys):
+    """The largest input the top-16 path takes on blocks of block_keys
+    keys: 2^16 segments of a uniform input within a block, with a five-sigma
+    margin."""
     import math
-    local = 256 * 18                                   # keys of a local-sort block (gfx950 build)
-    limit = (local - 5 * math.isqrt(local)) << 16
-    for n, expect in ((limit, 3), (limit + 1, 1)):
+    return (block_keys - 5 * math.isqrt(block_keys)) << 16
+
+
+def test_top16_size_limit(sorter):
+    """The largest input the top-16 path sorts on its 4,608-key local-sort
+    blocks (gfx950 build: 256 x 18) and one key more (the wide 9,216-key
+    blocks), the largest it sorts on those and one key more (the fused LSD
+    passes): ascending, same multiset."""
+    limit, wlimit = top16_limits(256 * 18), top16_limits(512 * 18)
+    assert (limit, wlimit) == (280_035_328, 572_522_496)
+    for n, expect in ((limit, 3), (limit + 1, 3), (wlimit, 3), (wlimit + 1, 1)):
         keys = datagen.uniform_u32(n, seed=980)
         k64 = keys.astype(np.uint64)
         s_sum, s_xor = int(k64.sum()), int(np.bitwise_xor.reduce(keys))
@@ -520,14 +528,13 @@ def test_top16_size_limit(sorter):
 
 
 def test_top16_size_limit_64(sorter):
-    """The same for u64 keys: the largest input the top-16 path takes by size
-    (2,304-key blocks of the 64-bit local sort) and one key more (the fused
-    LSD passes): ascending, same multiset."""
-    import math
-    local = 256 * 9                                    # keys of a 64-bit local-sort block (gfx950 build)
-    limit = (local - 5 * math.isqrt(local)) << 16
+    """The same for u64 keys: 2,304-key blocks of the 64-bit local sort
+    (256 x 9), then the wide 4,608-key blocks, then the fused LSD passes:
+    ascending, same multiset."""
+    limit, wlimit = top16_limits(256 * 9), top16_limits(512 * 9)
+    assert (limit, wlimit) == (135_266_304, 280_035_328)
     g = np.random.Generator(np.random.PCG64(981))
-    for n, expect in ((limit, 3), (limit + 1, 1)):
+    for n, expect in ((limit, 3), (limit + 1, 3), (wlimit, 3), (wlimit + 1, 1)):
         keys = g.integers(0, 1 << 64, size=n, dtype=np.uint64, endpoint=False)
         s_sum = int(np.bitwise_xor.reduce(keys)), int((keys & np.uint64(0xFFFFFFFF)).sum()), int((keys >> np.uint64(32)).sum())
         buf = sorter.alloc_sort_buffer("u64", n)
@@ -541,6 +548,33 @@ def test_top16_size_limit_64(sorter):
         assert (int(np.bitwise_xor.reduce(out)), int((out & np.uint64(0xFFFFFFFF)).sum()),
                 int((out >> np.uint64(32)).sum())) == s_sum
         del out
+
+
+WIDE_CASES = [(100, "uniform", 3), (4097, "uniform", 3), (1_000_003, "uniform", 3), (3_000_000, "few", 3),
+              (2_000_000, "dup", 3), (3_000_000, "top8", 3), (2_000_000, "grp2", 4), (16_777_216, "uniform", 3)]
+
+
+@pytest.mark.parametrize("kind", ["u32", "i32", "u64", "i64"])
+@pytest.mark.parametrize("n,dist,expect", WIDE_CASES)
+def test_top16_wide_blocks(sorter, kind, n, dist, expect):
+    """The top-16 path with its wide local-sort blocks (512 threads, which
+    inputs beyond the other blocks' size limit take), forced at every size:
+    exact against the oracle through the slice and buffer APIs; segments
+    that are tiny, larger than a block (two top-byte values), full of equal
+    keys; a re-scattered region."""
+    from forge_sort import TEST_LOCAL_WIDE, TEST_TOP16, TOP16_ALWAYS, TOP16_BY_SIZE
+    keys = make_keys(kind, n, dist, seed=995 + n % 83,
+                     tile=sorter.tile_config()["k64" if BITS[kind] == np.uint64 else "k32"])
+    sorter.set_test_option(TEST_TOP16, TOP16_ALWAYS)
+    sorter.set_test_option(TEST_LOCAL_WIDE, 1)
+    try:
+        check_sort(sorter, kind, keys)
+        assert sorter.first_pass() == expect
+        check_buffer(sorter, kind, keys)
+        assert sorter.first_pass() == expect
+    finally:
+        sorter.set_test_option(TEST_LOCAL_WIDE, 0)
+        sorter.set_test_option(TEST_TOP16, TOP16_BY_SIZE)
 
 
 def test_fused_first_pass_2_31_keys(sorter):

@@ -146,10 +146,12 @@ def test_perf_device(sorter, case, seed, floor):
 
 # (key type, n, floor in Mkeys/s): keys-only sorts on the top-16 path at sizes
 # between powers of two, where the segment bits must still keep a uniform
-# input's segments within a block (floors about half the rates measured on
-# one MI355X: u32 100M 111,900, 200M 128,300; u64 50M 66,000, 100M 74,000)
-BETWEEN_CASES = [("u32", 100_000_000, 55000.0), ("u32", 200_000_000, 64000.0),
-                 ("u64", 50_000_000, 33000.0), ("u64", 100_000_000, 37000.0)]
+# input's segments within a block, and beyond the 4,608- and 2,304-key
+# blocks' size limits (the wide blocks); floors about half the rates
+# measured on one MI355X: u32 100M 111,900, 200M 128,300, 400M 134,900;
+# u64 50M 66,000, 100M 74,000, 200M 74,800
+BETWEEN_CASES = [("u32", 100_000_000, 55000.0), ("u32", 200_000_000, 64000.0), ("u32", 400_000_000, 65000.0),
+                 ("u64", 50_000_000, 33000.0), ("u64", 100_000_000, 37000.0), ("u64", 200_000_000, 37000.0)]
 
 
 @pytest.mark.parametrize("kind,n,floor", BETWEEN_CASES)
