@@ -642,6 +642,22 @@ def test_config4_64bit(sorter, kind):
         check_buffer(sorter, "u64", datagen.low20_u64(n, high=0xABCDEF01234, seed=111))
 
 
+@pytest.mark.parametrize("kind,n", [("u32", 100_000_003), ("i32", 150_000_001), ("u64", 50_000_017),
+                                    ("i64", 3_000_001), ("u64", 200_000_003)])
+def test_top16_between_powers_of_two(sorter, kind, n):
+    """The top-16 path at sizes that are not powers of two (segment bits
+    chosen so that a uniform input's segments fit a block; u64 200M on the
+    wide blocks): exact against the oracle."""
+    if kind.endswith("32"):
+        keys = datagen.uniform_u32(n, seed=990 + n % 13)
+        keys = keys.view(np.int32) if kind == "i32" else keys
+    else:
+        keys = datagen.uniform_u64(n, seed=991 + n % 13)
+        keys = keys.view(np.int64) if kind == "i64" else keys
+    check_buffer(sorter, kind, keys)
+    assert sorter.first_pass() == 3
+
+
 @pytest.mark.parametrize("kind,n,dist", [
     ("u32", 1 << 28, "below 2^24"), ("i32", 1 << 28, "[-2^23, 2^23)"),
     ("u64", 1 << 27, "below 2^40"), ("u64", 1 << 27, "below 2^48")])
