@@ -303,6 +303,9 @@ WAVE_SERIAL_CASES = [
     "fused:u32:4000:uniform:4", "top16:u32:3000:uniform:5", "top16s12:u32:4000:uniform:6",
     "top16:u64:3000:uniform:7", "top16:u64:1500:few:8", "top16auto_lsd:u32:9000:zipf:9",
     "top16w:u32:3000:uniform:10", "top16w:u64:1500:few:11",
+    # 64-bit LSD passes in the top-16 sequence's slots, the last three on the
+    # persistent loop kernel (a tile loop with a barrier between tiles)
+    "top16auto_lsd:u64:20000:top8:12",
 ]
 
 
