@@ -1002,21 +1002,24 @@ def test_graph_capture_replays(hip_stream, op):
         s.close()
 
 
+@pytest.mark.parametrize("wide", [False, True], ids=["blocks", "wide_blocks"])
 @pytest.mark.parametrize("kind", ["u32", "u64"])
-def test_graph_capture_replays_top16(hip_stream, kind):
+def test_graph_capture_replays_top16(hip_stream, kind, wide):
     """The top-16 launch sequence captured once and replayed on new data: the
     region sample inside the graph picks, per replay, the top-16 path
     (uniform keys; a region overflow re-scattered; many equal keys, whose
     64-bit segments go to the deferred launch) or the LSD passes in the same
     launches (two top-byte values), or nothing after the fused pass (equal
-    keys); eager sorts run between the replays; every replay is exact."""
+    keys); eager sorts run between the replays; every replay is exact.  Also
+    with the wide local-sort blocks (the sizes beyond the others' limit)."""
     import ctypes
-    from forge_sort import TEST_TOP16, TOP16_SAMPLED, OP_SORT, GpuSorter
+    from forge_sort import TEST_LOCAL_WIDE, TEST_TOP16, TOP16_SAMPLED, OP_SORT, GpuSorter
     hip = ctypes.CDLL("libamdhip64.so.7")
     st = ctypes.c_void_p(hip_stream)
     s = GpuSorter.with_context(0, hip_stream)
     graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
     s.set_test_option(TEST_TOP16, TOP16_SAMPLED)       # the sample chooses at this size
+    s.set_test_option(TEST_LOCAL_WIDE, 1 if wide else 0)
     try:
         n, n_other = 1_500_007, 200_001
         tile = s.tile_config()["k64" if kind == "u64" else "k32"]
