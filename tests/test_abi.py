@@ -86,3 +86,7 @@ def test_python_constants_match_the_header():
     assert forge_sort.TOP16_MIN_KEYS32 == val("FS_TOP16_MIN_KEYS32")
     assert forge_sort.TOP16_MIN_KEYS64 == val("FS_TOP16_MIN_KEYS64")
     assert forge_sort.NO_ALLOC_MAX_KEYS == val("FS_NO_ALLOC_MAX_KEYS")
+    # the test options' numbers (enum fs_test_option)
+    opt = lambda name: int(re.search(r"\b%s = (\d+)" % name, h).group(1))
+    for name in ("WIDE_LOOKBACK", "UPSWEEP_BLOCKS_PER_CU", "INJECT_FAULT", "FUSED", "TOP16", "SEG_BITS", "LOCAL_WIDE"):
+        assert getattr(forge_sort, "TEST_" + name) == opt("FS_TEST_" + name), name
