@@ -44,13 +44,17 @@ const char* const kKernelNames[] = {
     "fs_scratch_address", "fs_first_k32", "fs_first_k64", "fs_region_sample_k32", "fs_region_sample_k64",
     "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_local_k64",
     "fs_local_deferred_k64", "fs_onesweep_loop_k64", "fs_local_deferred_k32", "fs_local_k32_w",
-    "fs_local_deferred_k32_w", "fs_local_k64_w", "fs_local_deferred_k64_w",
+    "fs_local_deferred_k32_w", "fs_local_k64_w", "fs_local_deferred_k64_w", "fs_onesweep_k32_s",
+    "fs_onesweep_any_k32_s",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
     K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOCAL64, K_DEFER64, K_LOOP64, K_DEFER32,
-    K_LOCAL32W, K_DEFER32W, K_LOCAL64W, K_DEFER64W, K_COUNT
+    K_LOCAL32W, K_DEFER32W, K_LOCAL64W, K_DEFER64W, K_OS32S, K_ANY32S, K_COUNT
 };
+// the stable digit-pass kernel and the keys-only first-pass kernel of each variant (FS_VAR_*)
+const int kPassKernel[FS_VARIANTS] = {K_OS32, K_OS32V, K_OS64, K_OS64V, K_OS32S};
+const int kAnyKernel[FS_VARIANTS] = {K_ANY32, -1, K_ANY64, -1, K_ANY32S};
 
 }  // namespace
 
@@ -60,8 +64,8 @@ struct fs_sorter {
     bool own_stream = false;
     hipModule_t module = nullptr;
     hipFunction_t fn[K_COUNT] = {};
-    uint32_t tile[4] = {};          // keys per tile of each digit-pass variant (FS_VAR_*)
-    uint32_t block[4] = {};         // threads per block of each variant
+    uint32_t tile[FS_VARIANTS] = {};    // keys per tile of each digit-pass variant (FS_VAR_*)
+    uint32_t block[FS_VARIANTS] = {};   // threads per block of each variant
     // keys a block of the local sort holds and its threads per block, by
     // [wide][64-bit keys] (fs_local_k32, fs_local_k64, fs_local_k32_w, fs_local_k64_w)
     uint32_t local_keys[2][2] = {};
@@ -356,6 +360,16 @@ static bool top16_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
     return n >= (key64(t) ? FS_TOP16_MIN_KEYS64 : FS_TOP16_MIN_KEYS32) && n <= (local_mean_max(s, t, true) << 16);
 }
 
+// The digit-pass variant a sort runs: by key width and op, and the small
+// tiles (FS_VAR_K32S) for keys-only 32-bit sorts below FS_SMALL_TILE_KEYS keys
+// on the LSD passes (the fused and top-16 sequences and the static scratch
+// keep the stable tiles).
+static int sort_variant(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n, bool no_alloc) {
+    const int v = variant_of(op, t);
+    if (v != FS_VAR_K32 || no_alloc || n >= FS_SMALL_TILE_KEYS) return v;
+    return fused_path(s, op, t, n) || top16_path(s, op, t, n) ? v : FS_VAR_K32S;
+}
+
 // The top-16 path's local sort runs on wide blocks (twice the keys) where
 // the 2^16 segments of a uniform input would outgrow the other blocks.
 static bool local_wide(const fs_sorter* s, fs_key_type t, uint64_t n) {
@@ -381,7 +395,7 @@ static uint32_t seg_bits_for(uint64_t n, uint64_t mean_max) {
 static fs_status reserve(fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) {
     if (n <= 1) return FS_OK;
     const size_t kb = key_bytes(t);
-    const uint32_t tile = s->tile[variant_of(op, t)];
+    const uint32_t tile = s->tile[sort_variant(s, op, t, n, false)];
     const uint64_t num_tiles = (n + tile - 1) / tile;
     fs_status r;
     const bool fused = fused_path(s, op, t, n) || top16_path(s, op, t, n);
@@ -448,7 +462,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
     const size_t kb = key_bytes(t);
     if ((uintptr_t)keys % kb != 0 || (vals && (uintptr_t)vals % 4 != 0))
         return set_err(s, FS_ERR_INVALID_ARGUMENT, "misaligned key or value pointer");
-    const int var = variant_of(op, t);
+    const int var = sort_variant(s, op, t, n, no_alloc);
     const uint32_t tile = s->tile[var];
     const uint32_t num_tiles = (uint32_t)((n + tile - 1) / tile);
     // the static scratch holds narrow look-back entries (n < 2^30 there)
@@ -567,7 +581,7 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
             // whose top 16 bits the sample refused) take the loop kernel's
             // small grid (idle: ~5 µs; working: one block per CU, slower).
             const bool loop = top16 && key64(t) && sl >= FS_LOOP_SLOT64;
-            if ((r = launch(s, loop ? K_LOOP64 : K_OS32 + var, loop ? small : num_tiles, s->block[var], args2, st,
+            if ((r = launch(s, loop ? K_LOOP64 : kPassKernel[var], loop ? small : num_tiles, s->block[var], args2, st,
                             no_alloc)) != FS_OK)
                 return r;
         }
@@ -592,13 +606,13 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         const unsigned up_grid = (unsigned)up_blocks;
         if ((r = launch(s, key64(t) ? K_UP64 : K_UP32, up_grid, FS_HIST_BLOCK, args1, st, no_alloc)) != FS_OK) return r;
     }
-    const int os = K_OS32 + var;   // kernel order matches FS_VAR_*
+    const int os = kPassKernel[var];
     for (uint32_t d = 0; d < a.digits; ++d) {
         uint32_t digit = d;
         void* args2[] = {&a, &digit};
         // digit 0 of a keys-only sort: its pass, when it runs, is the first,
         // which needs no stability (same tiles as the stable kernel)
-        const int k = (d == 0 && op == FS_OP_SORT) ? (key64(t) ? K_ANY64 : K_ANY32) : os;
+        const int k = (d == 0 && op == FS_OP_SORT) ? kAnyKernel[var] : os;
         unsigned grid = num_tiles;
 #ifdef FS_FAULT_INJECTION
         if (s->fault == FS_FAULT_EXTRA_BLOCK && d == 0) grid += 1u;
@@ -703,13 +717,14 @@ static fs_status create(int device, hipStream_t stream, bool own, fs_sorter** ou
         // tile geometry compiled into the code object
         hipDeviceptr_t gp = nullptr, bp = nullptr;
         size_t gsz = 0, bsz = 0;
-        if (hipModuleGetGlobal(&gp, &gsz, s->module, "fs_kernel_tile_keys") != hipSuccess || gsz != 16 ||
-            hipModuleGetGlobal(&bp, &bsz, s->module, "fs_kernel_block_threads") != hipSuccess || bsz != 16 ||
-            hipMemcpyDtoH(s->tile, gp, 16) != hipSuccess || hipMemcpyDtoH(s->block, bp, 16) != hipSuccess) {
+        if (hipModuleGetGlobal(&gp, &gsz, s->module, "fs_kernel_tile_keys") != hipSuccess || gsz != sizeof s->tile ||
+            hipModuleGetGlobal(&bp, &bsz, s->module, "fs_kernel_block_threads") != hipSuccess ||
+            bsz != sizeof s->block || hipMemcpyDtoH(s->tile, gp, sizeof s->tile) != hipSuccess ||
+            hipMemcpyDtoH(s->block, bp, sizeof s->block) != hipSuccess) {
             return create_failed(s, FS_ERR_SHADER_COMPILATION,
                                  "code object lacks fs_kernel_tile_keys/fs_kernel_block_threads");
         }
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FS_VARIANTS; ++i)
             if (s->tile[i] == 0 || s->block[i] < FS_RADIX)
                 return create_failed(s, FS_ERR_SHADER_COMPILATION, "code object has an invalid tile geometry");
         hipDeviceptr_t lp = nullptr;

@@ -44,11 +44,31 @@
 #ifndef FS_STAGE_BATCH
 #define FS_STAGE_BATCH 8
 #endif
+// Small tiles of the keys-only 32-bit digit pass: keys-only u32/i32/f32 sorts
+// below FS_SMALL_TILE_KEYS keys on the LSD passes (not the fused or top-16
+// launch sequences, whose kernels share the tiles above, nor the static
+// scratch of fs_encode_no_alloc, laid out for them).  Below 2^21 keys a pass
+// has too few 768 x 23-key tiles to fill the CUs.  u32 sorts (host-timed
+// median, µs) with 768 x 12 / 8 / 6-key tiles: 65,536 keys 62.9 / 58.8 /
+// 59.2, 2^18 66.0 / 62.8 / 61.6, 2^20 75.9 / 73.1 / 73.2, 2^21 - 1 87.6 /
+// 90.1 / 91.0; 768 x 23 at 2^20 87.0, at 2^21 96.2 (from 2^23 keys on the
+// larger tiles are faster).
+#ifndef FS_K32S_BLOCK
+#define FS_K32S_BLOCK 768
+#endif
+#ifndef FS_K32S_ITEMS
+#define FS_K32S_ITEMS 8
+#endif
+#ifndef FS_SMALL_TILE_KEYS
+#define FS_SMALL_TILE_KEYS (1u << 21)
+#endif
 // index into fs_kernel_tile_keys
 #define FS_VAR_K32 0
 #define FS_VAR_K32V 1
 #define FS_VAR_K64 2
 #define FS_VAR_K64V 3
+#define FS_VAR_K32S 4
+#define FS_VARIANTS 5
 
 // Histogram atomics: a wave whose lanes share one digit with at least
 // FS_PEEL_MIN others adds that digit's lanes with one atomic.

@@ -368,6 +368,8 @@ void fs_local_k32(FsArgs);
 void fs_local_k64(FsArgs);
 void fs_local_deferred_k64(FsArgs);
 void fs_local_deferred_k32(FsArgs);
+void fs_onesweep_k32_s(FsArgs, uint32_t);
+void fs_onesweep_any_k32_s(FsArgs, uint32_t);
 void fs_local_k32_w(FsArgs);
 void fs_local_deferred_k32_w(FsArgs);
 void fs_local_k64_w(FsArgs);
@@ -380,8 +382,8 @@ void fs_region_sample_k64(FsArgs);
 void fs_iota(uint32_t*, uint64_t);
 void fs_scratch_address(uint64_t*);
 void fs_gather_elems(uint64_t, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint64_t);
-extern uint32_t fs_kernel_tile_keys[4];
-extern uint32_t fs_kernel_block_threads[4];
+extern uint32_t fs_kernel_tile_keys[FS_VARIANTS];
+extern uint32_t fs_kernel_block_threads[FS_VARIANTS];
 extern uint32_t fs_kernel_local_geometry[9];
 }
 
@@ -407,6 +409,8 @@ static emu_function g_funcs[] = {
     {"fs_local_k64", [](void** p) { fs_local_k64(A0); }},
     {"fs_local_deferred_k64", [](void** p) { fs_local_deferred_k64(A0); }},
     {"fs_local_deferred_k32", [](void** p) { fs_local_deferred_k32(A0); }},
+    {"fs_onesweep_k32_s", [](void** p) { fs_onesweep_k32_s(A0, D1); }},
+    {"fs_onesweep_any_k32_s", [](void** p) { fs_onesweep_any_k32_s(A0, D1); }},
     {"fs_local_k32_w", [](void** p) { fs_local_k32_w(A0); }},
     {"fs_local_deferred_k32_w", [](void** p) { fs_local_deferred_k32_w(A0); }},
     {"fs_local_k64_w", [](void** p) { fs_local_k64_w(A0); }},

@@ -172,6 +172,19 @@ def test_sort_sizes(sorter, kind, n):
     check_sort(sorter, kind, make_keys(kind, n, "uniform", seed=n))
 
 
+@pytest.mark.parametrize("kind", ["u32", "i32", "f32"])
+@pytest.mark.parametrize("n,dist", [((1 << 21) - 1, "uniform"), (1 << 21, "uniform"), ((1 << 21) - 1, "few"),
+                                    (1_500_001, "byte1"), (6_144 * 7 + 5, "uniform")])
+def test_small_tile_boundary(sorter, kind, n, dist):
+    """Keys-only 32-bit sorts take the digit pass's small tiles below 2^21
+    keys (FS_SMALL_TILE_KEYS) and the stable tiles from there: exact against
+    the oracle on both sides, a single varying digit (the copy and the pass
+    on the small tiles) and a ragged last tile."""
+    keys = make_keys(kind, n, dist, seed=140 + n % 91)
+    check_sort(sorter, kind, keys)
+    check_buffer(sorter, kind, keys)
+
+
 TILE_VARIANT = {("sort", False): "k32", ("sort", True): "k64", ("argsort", False): "k32_v",
                 ("argsort", True): "k64_v", ("pairs", False): "k32_v", ("pairs", True): "k64_v"}
 
