@@ -83,6 +83,11 @@ SMALL_CASES = [
     "sort:u32:9000:zipf:28", "pairs:u32:7000:zipf:29", "argsort:u64:3000:zipf:30",
     # several upsweep steps and counter folds per block
     "sort:u64:9000:uniform:37", "sort:u32:9000:same:38", "sort:i64:9000:zipf:39",
+    # keys-only 32-bit sorts on the small tiles (below 4096 keys in this
+    # build) and at the boundary; a fused first pass forced below it keeps
+    # the stable tiles
+    "sort:u32:4095:uniform:40", "sort:i32:4096:few:41", "sort:f32:3000:byte1:42", "sort:u32:3001:same:43",
+    "fused:u32:3000:uniform:44",
 ]
 
 PROD_CASES = [
