@@ -45,16 +45,17 @@ const char* const kKernelNames[] = {
     "fs_local_k32", "fs_rescatter_k32", "fs_rescatter_k64", "fs_local_k64",
     "fs_local_deferred_k64", "fs_onesweep_loop_k64", "fs_local_deferred_k32", "fs_local_k32_w",
     "fs_local_deferred_k32_w", "fs_local_k64_w", "fs_local_deferred_k64_w", "fs_onesweep_k32_s",
-    "fs_onesweep_any_k32_s",
+    "fs_onesweep_any_k32_s", "fs_onesweep_k32_vs", "fs_onesweep_k64_s", "fs_onesweep_any_k64_s", "fs_onesweep_k64_vs",
 };
 enum {
     K_UP32, K_UP64, K_OS32, K_OS32V, K_OS64, K_OS64V, K_IOTA, K_ANY32, K_ANY64, K_SCRATCH_ADDR, K_FIRST32, K_FIRST64,
     K_SAMPLE32, K_SAMPLE64, K_LOCAL32, K_RESCATTER32, K_RESCATTER64, K_LOCAL64, K_DEFER64, K_LOOP64, K_DEFER32,
-    K_LOCAL32W, K_DEFER32W, K_LOCAL64W, K_DEFER64W, K_OS32S, K_ANY32S, K_COUNT
+    K_LOCAL32W, K_DEFER32W, K_LOCAL64W, K_DEFER64W, K_OS32S, K_ANY32S, K_OS32VS, K_OS64S, K_ANY64S, K_OS64VS,
+    K_COUNT
 };
 // the stable digit-pass kernel and the keys-only first-pass kernel of each variant (FS_VAR_*)
-const int kPassKernel[FS_VARIANTS] = {K_OS32, K_OS32V, K_OS64, K_OS64V, K_OS32S};
-const int kAnyKernel[FS_VARIANTS] = {K_ANY32, -1, K_ANY64, -1, K_ANY32S};
+const int kPassKernel[FS_VARIANTS] = {K_OS32, K_OS32V, K_OS64, K_OS64V, K_OS32S, K_OS32VS, K_OS64S, K_OS64VS};
+const int kAnyKernel[FS_VARIANTS] = {K_ANY32, -1, K_ANY64, -1, K_ANY32S, -1, K_ANY64S, -1};
 
 }  // namespace
 
@@ -360,14 +361,15 @@ static bool top16_path(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n) 
     return n >= (key64(t) ? FS_TOP16_MIN_KEYS64 : FS_TOP16_MIN_KEYS32) && n <= (local_mean_max(s, t, true) << 16);
 }
 
-// The digit-pass variant a sort runs: by key width and op, and the small
-// tiles (FS_VAR_K32S) for keys-only 32-bit sorts below FS_SMALL_TILE_KEYS keys
-// on the LSD passes (the fused and top-16 sequences and the static scratch
-// keep the stable tiles).
+// The digit-pass variant a sort runs: by key width and op, and its small
+// tiles (FS_VAR_K32S ... FS_VAR_K64VS) below FS_SMALL_TILE_KEYS (32-bit keys)
+// or FS_SMALL_TILE_KEYS64 (64-bit keys) keys on the LSD passes (the fused and
+// top-16 sequences and the static scratch keep the larger tiles).
 static int sort_variant(const fs_sorter* s, fs_op op, fs_key_type t, uint64_t n, bool no_alloc) {
     const int v = variant_of(op, t);
-    if (v != FS_VAR_K32 || no_alloc || n >= FS_SMALL_TILE_KEYS) return v;
-    return fused_path(s, op, t, n) || top16_path(s, op, t, n) ? v : FS_VAR_K32S;
+    if (no_alloc || n >= (key64(t) ? FS_SMALL_TILE_KEYS64 : FS_SMALL_TILE_KEYS)) return v;
+    if (op == FS_OP_SORT && (fused_path(s, op, t, n) || top16_path(s, op, t, n))) return v;
+    return v + (FS_VAR_K32S - FS_VAR_K32);    // the small variant of each (FS_VAR_* order)
 }
 
 // The top-16 path's local sort runs on wide blocks (twice the keys) where

@@ -62,13 +62,37 @@
 #ifndef FS_SMALL_TILE_KEYS
 #define FS_SMALL_TILE_KEYS (1u << 21)
 #endif
+// The same for 32-bit argsort and pairs (768 x 6 below 2^21 keys), and for
+// 64-bit keys, with and without values (768 x 4 below FS_SMALL_TILE_KEYS64).
+// Host-timed medians, µs, large / small tiles: u32 argsort 2^16 keys 81 / 61,
+// 2^20 91 / 79, 2^21 - 1 100 / 93; u32 pairs 2^20 97 / 83, 2^21 - 1 104 / 95;
+// u64 sort 2^16 108 / 90, 2^18 117 / 100, 2^20 149 / 142, 2^21 - 1 174 / 198;
+// u64 argsort 2^18 125 / 106, 2^21 - 1 183 / 202; f64 pairs 2^18 128 / 108.
+#ifndef FS_K32VS_ITEMS
+#define FS_K32VS_ITEMS 6
+#endif
+#ifndef FS_K64S_ITEMS
+#define FS_K64S_ITEMS 4
+#endif
+#ifndef FS_K64VS_ITEMS
+#define FS_K64VS_ITEMS 4
+#endif
+#ifndef FS_KS_BLOCK
+#define FS_KS_BLOCK 768
+#endif
+#ifndef FS_SMALL_TILE_KEYS64
+#define FS_SMALL_TILE_KEYS64 (1u << 20)
+#endif
 // index into fs_kernel_tile_keys
 #define FS_VAR_K32 0
 #define FS_VAR_K32V 1
 #define FS_VAR_K64 2
 #define FS_VAR_K64V 3
-#define FS_VAR_K32S 4
-#define FS_VARIANTS 5
+#define FS_VAR_K32S 4      // the small tiles of each of the four
+#define FS_VAR_K32VS 5
+#define FS_VAR_K64S 6
+#define FS_VAR_K64VS 7
+#define FS_VARIANTS 8
 
 // Histogram atomics: a wave whose lanes share one digit with at least
 // FS_PEEL_MIN others adds that digit's lanes with one atomic.

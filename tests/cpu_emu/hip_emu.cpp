@@ -370,6 +370,10 @@ void fs_local_deferred_k64(FsArgs);
 void fs_local_deferred_k32(FsArgs);
 void fs_onesweep_k32_s(FsArgs, uint32_t);
 void fs_onesweep_any_k32_s(FsArgs, uint32_t);
+void fs_onesweep_k32_vs(FsArgs, uint32_t);
+void fs_onesweep_k64_s(FsArgs, uint32_t);
+void fs_onesweep_any_k64_s(FsArgs, uint32_t);
+void fs_onesweep_k64_vs(FsArgs, uint32_t);
 void fs_local_k32_w(FsArgs);
 void fs_local_deferred_k32_w(FsArgs);
 void fs_local_k64_w(FsArgs);
@@ -411,6 +415,10 @@ static emu_function g_funcs[] = {
     {"fs_local_deferred_k32", [](void** p) { fs_local_deferred_k32(A0); }},
     {"fs_onesweep_k32_s", [](void** p) { fs_onesweep_k32_s(A0, D1); }},
     {"fs_onesweep_any_k32_s", [](void** p) { fs_onesweep_any_k32_s(A0, D1); }},
+    {"fs_onesweep_k32_vs", [](void** p) { fs_onesweep_k32_vs(A0, D1); }},
+    {"fs_onesweep_k64_s", [](void** p) { fs_onesweep_k64_s(A0, D1); }},
+    {"fs_onesweep_any_k64_s", [](void** p) { fs_onesweep_any_k64_s(A0, D1); }},
+    {"fs_onesweep_k64_vs", [](void** p) { fs_onesweep_k64_vs(A0, D1); }},
     {"fs_local_k32_w", [](void** p) { fs_local_k32_w(A0); }},
     {"fs_local_deferred_k32_w", [](void** p) { fs_local_deferred_k32_w(A0); }},
     {"fs_local_k64_w", [](void** p) { fs_local_k64_w(A0); }},

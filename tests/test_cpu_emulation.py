@@ -88,6 +88,10 @@ SMALL_CASES = [
     # the stable tiles
     "sort:u32:4095:uniform:40", "sort:i32:4096:few:41", "sort:f32:3000:byte1:42", "sort:u32:3001:same:43",
     "fused:u32:3000:uniform:44",
+    # argsort / pairs on the small 32-bit tiles, 64-bit sorts on theirs
+    # (below 2048 keys in this build) and at that boundary
+    "argsort:f32:4095:uniform:45", "pairs:u32:4096:few:46", "sort:i64:2047:few:47", "pairs:f64:2047:uniform:48",
+    "argsort:u64:2048:uniform:49",
 ]
 
 PROD_CASES = [

@@ -185,6 +185,21 @@ def test_small_tile_boundary(sorter, kind, n, dist):
     check_buffer(sorter, kind, keys)
 
 
+@pytest.mark.parametrize("kind", ["u32", "f32", "u64", "i64", "f64"])
+def test_small_tile_boundary_values_and_64(sorter, kind):
+    """Argsort and pairs below and at FS_SMALL_TILE_KEYS (32-bit keys), and
+    64-bit sorts, argsort and pairs below and at FS_SMALL_TILE_KEYS64 (2^20):
+    exact against the oracle on both tile sizes."""
+    limit = (1 << 20) if kind.endswith("64") else (1 << 21)
+    for n in (limit - 1, limit):
+        keys = make_keys(kind, n, "few" if n % 2 else "uniform", seed=150 + n % 89)
+        if kind.endswith("64"):
+            check_sort(sorter, kind, keys)
+        check_argsort(sorter, kind, keys)
+        vals = np.random.Generator(np.random.PCG64(n)).integers(0, 1 << 32, size=n, dtype=np.uint32)
+        check_pairs(sorter, kind, keys, vals)
+
+
 TILE_VARIANT = {("sort", False): "k32", ("sort", True): "k64", ("argsort", False): "k32_v",
                 ("argsort", True): "k64_v", ("pairs", False): "k32_v", ("pairs", True): "k64_v"}
 
