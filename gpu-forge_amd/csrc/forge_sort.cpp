@@ -595,7 +595,8 @@ static fs_status enqueue(fs_sorter* s, fs_op op, fs_key_type t, void* keys, uint
         // the segments the local sort deferred (larger than a block; 64-bit
         // keys: many equal keys; 32-bit keys: fewer segment bits than it
         // sorts in one stable pass), on a small grid
-        if (top16 && (r = launch(s, kdefer, small, lthreads, args1, st, no_alloc)) != FS_OK)
+        if (top16 && (r = launch(s, kdefer, small, key64(t) ? FS_LD64_BLOCK : FS_LD32_BLOCK, args1, st, no_alloc)) !=
+                         FS_OK)
             return r;
         s->last_stream = st;
         s->pending = true;

@@ -332,6 +332,18 @@
 #ifndef FS_L64_GLIM
 #define FS_L64_GLIM 32u
 #endif
+// Threads per block of the local sort's deferred launches (the same keys per
+// thread, one block per CU): segments up to that many times the keys per
+// thread are sorted in LDS there, larger ones a digit at a time through
+// scratch.  (Inputs with many copies of each key make segments of a few
+// values times their copies: at 2^28 u32 keys with 2^16 distinct values,
+// 2-4 times a block of the first launch.)
+#ifndef FS_LD32_BLOCK
+#define FS_LD32_BLOCK 512
+#endif
+#ifndef FS_LD64_BLOCK
+#define FS_LD64_BLOCK 1024
+#endif
 // Wide local-sort blocks (the same keys per thread, FS_LW_BLOCK threads):
 // sorts too large for 2^16 segments of the blocks above to fit them (more
 // than 280M 32-bit or 135M 64-bit keys) take the top-16 path on these, up

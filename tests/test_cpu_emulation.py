@@ -282,6 +282,11 @@ TOP16_SMALL = [
     "top16s12:i64:20000:uniform:43",
     "top16auto:u64:20000:uniform:44", "top16auto_lsd:u64:20000:top8:45", "top16auto_lsdover:i64:30000:top8grp0:46",
     "top16auto_lsd:u64:9000:low12:47",
+    # 64-bit segments with many copies of each key: groups of equal keys
+    # above the comparison limit ranked by slot (first launch and deferred
+    # launch); a large group of different keys in a block-sized segment
+    # (the group sort gives way to LSD in LDS in the deferred launch)
+    "top16:u64:20000:few:60", "top16:u64:400:low12:61", "top16:i64:500:low12:62",
     # the wide local-sort blocks (FS_LW_BLOCK threads, which sorts beyond the
     # other blocks' size limit take): both key widths, every local plan,
     # equal keys (64-bit LSD fallback in LDS), a re-scattered region
@@ -315,6 +320,9 @@ WAVE_SERIAL_CASES = [
     # 64-bit LSD passes in the top-16 sequence's slots, the last three on the
     # persistent loop kernel (a tile loop with a barrier between tiles)
     "top16auto_lsd:u64:20000:top8:12",
+    # the deferred launches: group sort giving way to LSD in LDS, and big
+    # segments of equal keys
+    "top16:u64:400:low12:13", "top16:u64:3000:few:14", "top16:u32:3000:few:15",
 ]
 
 
