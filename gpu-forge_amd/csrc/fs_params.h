@@ -316,7 +316,8 @@
 #ifndef FS_L32_ITEMS
 #define FS_L32_ITEMS 18
 #endif
-// 64-bit keys: 256 x 9 keys per block (an 18 KiB stage, 26 KiB of LDS: six blocks per CU)
+// 64-bit keys: 256 x 9 keys per block (an 18 KiB stage holding the group counters
+// until it is written, 22 KiB of LDS: seven blocks per CU)
 #ifndef FS_L64_BLOCK
 #define FS_L64_BLOCK 256
 #endif
